@@ -1,0 +1,200 @@
+"""Benchmark of the paged-attention path on one MI355X.
+
+A step is one attention layer of one engine tick: the fused q/k RMSNorm +
+RoPE + KV append of the step's tokens, then paged attention over the page
+table. The headline workload is batched decode (batch 32, contexts uniform
+in [256, 4096], 262,144-token pool); consecutive steps use different layers
+of an 8-layer pool, as the 36 layers of a forward pass do, so the 256 MB
+MALL cannot serve the K/V bytes. value = algorithmic bytes of a step
+(every K/V row of every context once + q/out rows + appended rows) divided
+by the measured step time, in GB/s.
+
+The JSON line also carries the other four workloads (GPU timing only), the
+roofline of the dominant kernel (decode attention; its average duration is
+measured with HIP events on the launch stream over the timed steps) and a
+CPU baseline: the oracle's decode attention timed on the host, one thread,
+on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "hayate-exp_amd"))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+METRIC = "decode attn HBM GB/s & prefill attn TFLOP/s (% of MI355X peak), Qwen3-4B"
+EPS = 1e-6
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def step_fn(w, batch, layer):
+    q_rot = batch.norm_rope_write_layer(layer, w.q, w.k, w.v, w.q_norm_w, w.k_norm_w, EPS,
+                                        w.cos, w.sin)
+    return q_rot
+
+
+def time_workload(name, steps, warmup, layers, split=0):
+    """Times `steps` steps; returns a dict of measurements."""
+    from hayate_amd.workloads import make_workload
+
+    w = make_workload(name, device="cuda", num_layers=layers, tokens_per_split=split)
+    batch = w.begin()
+    stream = torch.cuda.current_stream()
+    plan = batch.plan(w.q.shape[1])
+    for i in range(warmup):
+        q_rot = step_fn(w, batch, i % layers)
+        batch.attend_layer(q_rot, i % layers)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        layer = i % layers
+        q_rot = step_fn(w, batch, layer)
+        ev[i][0].record(stream)
+        batch.attend_layer(q_rot, layer)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    attn_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    step_ms = (t1 - t0) * 1e3 / steps
+    out = {
+        "workload": w.spec.description,
+        "ms_per_step": step_ms,
+        "attn_ms": attn_ms,
+        "decode_bytes": w.decode_bytes(),
+        "prefill_flops": w.prefill_flops(),
+        "n_decode_items": plan.n_decode,
+        "n_prefill_items": plan.n_prefill,
+    }
+    if out["decode_bytes"]:
+        out["decode_GBps_step"] = out["decode_bytes"] / (step_ms * 1e-3) / 1e9
+        out["decode_GBps_attn"] = out["decode_bytes"] / (attn_ms * 1e-3) / 1e9
+        out["decode_frac_hbm"] = out["decode_GBps_attn"] / HBM_PEAK_GBS
+    if out["prefill_flops"]:
+        out["prefill_TFLOPs_attn"] = out["prefill_flops"] / (attn_ms * 1e-3) / 1e12
+        out["prefill_frac_mfma"] = out["prefill_TFLOPs_attn"] / BF16_PEAK_TFLOPS
+    del w, batch
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(budget_s=10.0):
+    """Oracle decode attention on the host, 1 thread, over as many requests
+    of the batch-32 decode workload as fit in about `budget_s` seconds."""
+    from threadpoolctl import threadpool_limits
+
+    from hayate_amd.workloads import make_workload
+    from oracle import paged_ref as R
+
+    w = make_workload("decode_b32", device="cuda", num_layers=1)
+    pk = R.torch_bf16_to_bits(w.manager.k_cache[0, 0])
+    pv = R.torch_bf16_to_bits(w.manager.v_cache[0, 0])
+    q = R.torch_bf16_to_bits(w.q)
+    done_bytes = 0
+    n = 0
+    torch.set_num_threads(1)
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        while n < len(w.q_lens) and time.perf_counter() - t0 < budget_s:
+            R.paged_attention(q[n : n + 1], pk, pv, [w.page_lists[n]], [w.cache_lens[n]], [1],
+                              128, dtype=np.float32)
+            done_bytes += (w.cache_lens[n] + 1) * 4096
+            n += 1
+        dt = time.perf_counter() - t0
+    return {
+        "value": done_bytes / dt / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"oracle float32 paged decode attention over the first {n} of 32 "
+                  f"requests of the batch-32 decode workload ({dt:.1f} s)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--split", type=int, default=0, help="decode tokens per split (0 = auto)")
+    ap.add_argument("--only", default="", help="comma-separated workloads (default: all)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the paged-attention path runs on one "
+              "MI355X; multi-GPU runs are not part of this build.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        sys.exit(1)
+
+    from hayate_amd.workloads import ORDER
+
+    names = [n for n in ORDER if not args.only or n in args.only.split(",")]
+    if "decode_b32" not in names:
+        names.append("decode_b32")
+    results = {}
+    for name in names:
+        log(f"[bench] {name}")
+        results[name] = time_workload(name, args.steps, args.warmup, args.layers, args.split)
+        log(f"[bench] {name}: {json.dumps(results[name])}")
+
+    head = results["decode_b32"]
+    line = {
+        "metric": METRIC,
+        "value": round(head["decode_GBps_step"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode_b32: batched paged decode, batch 32, contexts U[256, 4096], "
+                        "262,144-token pool, 128-token pages, 32 q / 8 kv heads, head_dim 128; "
+                        f"step = fused qk-norm+rope+append + decode attention, {args.layers} "
+                        "layers rotated",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(head["decode_GBps_attn"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(head["decode_frac_hbm"], 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        line["cpu_baseline"] = cpu_baseline()
+    line["configs"] = {
+        n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+        for n, r in results.items()
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

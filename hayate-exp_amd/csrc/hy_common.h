@@ -1,0 +1,113 @@
+// Shared device helpers and host-side error plumbing for libhayate_attn.
+// Target: gfx950 (CDNA4), wave64.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hayate_attn.h"
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting (thread-local message, negative return codes).
+// ---------------------------------------------------------------------------
+namespace hy {
+
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Checks the launch status of the kernels just enqueued.
+int launch_status(const char *what);
+
+}  // namespace hy
+
+#define HY_REQUIRE(cond, ...)          \
+  do {                                 \
+    if (!(cond)) {                     \
+      hy::set_error(__VA_ARGS__);      \
+      return HY_EINVAL;                \
+    }                                  \
+  } while (0)
+
+#define HY_REQUIRE_SUPPORTED(cond, ...) \
+  do {                                  \
+    if (!(cond)) {                      \
+      hy::set_error(__VA_ARGS__);       \
+      return HY_EUNSUPPORTED;           \
+    }                                   \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+namespace hy {
+
+constexpr int kHeadDim = 128;  // Qwen3 head_dim; the kernels are built for it.
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 stored as raw uint16; widening is exact.
+__device__ __forceinline__ float bf16_lo(uint32_t w) {
+  return __uint_as_float(w << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t w) {
+  return __uint_as_float(w & 0xffff0000u);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// fp32 -> bf16 round-to-nearest-even, NaN -> 0x7fc0 (the rule torch's
+// c10::BFloat16 conversion uses), written out so results are bit-exact.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+}
+
+// 16-byte global load / store of 8 bf16 values.
+__device__ __forceinline__ u32x4 load16(const void *p) {
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+__device__ __forceinline__ void store16(void *p, u32x4 v) {
+  *reinterpret_cast<u32x4 *>(p) = v;
+}
+
+// Broadcast lane `src` of every 16-lane row to the whole row (DPP
+// row_newbcast, gfx90a and later).
+template <int src>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(
+      0, __float_as_int(x), 0x150 + src, 0xf, 0xf, false));
+}
+
+// Sum / max over the 16 lanes of a row (xor butterfly).
+__device__ __forceinline__ float row16_sum(float x) {
+  x += __shfl_xor(x, 8, 16);
+  x += __shfl_xor(x, 4, 16);
+  x += __shfl_xor(x, 2, 16);
+  x += __shfl_xor(x, 1, 16);
+  return x;
+}
+
+// Sequence index owning packed token `tok` given cumulative q_start[0..n].
+__device__ __forceinline__ int find_seq(const int32_t *__restrict__ q_start,
+                                        int num_seqs, int tok) {
+  int lo = 0, hi = num_seqs - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (q_start[mid] <= tok)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+}  // namespace hy

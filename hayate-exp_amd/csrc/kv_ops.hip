@@ -1,0 +1,427 @@
+// Paged KV append, fused QK-RMSNorm + RoPE + append, page gather/scatter.
+//
+// Work decomposition: one 16-lane row group per 128-element head row; every
+// lane moves 8 bf16 (16 bytes), so a wave covers four head rows with fully
+// coalesced 256-byte row segments. These kernels are HBM-bound copies; no
+// LDS is used.
+//
+// Built with -ffp-contract=off: the norm and rotation must round each fp32
+// product and sum separately, as the reference's chain of elementwise torch
+// ops does (hayate/model/rope.py:44-47), so no FMA contraction is allowed.
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "hy_common.h"
+
+namespace hy {
+
+namespace {
+
+constexpr int kRowsPerBlock = 16;  // 256 threads = 16 head rows
+
+struct RowAddr {
+  int64_t seq, tok, head;
+};
+
+// Physical token index of logical position t of sequence b.
+__device__ __forceinline__ int64_t phys_token(const int32_t *__restrict__ pt,
+                                              int64_t pt_stride, int b, int t,
+                                              int page_size) {
+  const int page = pt[static_cast<int64_t>(b) * pt_stride + t / page_size];
+  return static_cast<int64_t>(page) * page_size + (t % page_size);
+}
+
+// ---------------------------------------------------------------------------
+// Plain append: pool[h, phys(b, c_b + i)] = src[b, i, h]  (K and V).
+// Row index r in [0, 2 * total_tokens * Hkv): first all K rows, then V rows.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void kv_append_kernel(
+    uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool,
+    int64_t pool_hs, const uint16_t *__restrict__ k, int64_t k_ss,
+    int64_t k_st, int64_t k_sh, const uint16_t *__restrict__ v, int64_t v_ss,
+    int64_t v_st, int64_t v_sh, const int32_t *__restrict__ q_start,
+    const int32_t *__restrict__ cache_lens,
+    const int32_t *__restrict__ page_table, int64_t pt_stride, int num_seqs,
+    int total_tokens, int num_kv_heads, int page_size) {
+  const int lane = threadIdx.x & 15;
+  const int64_t rows_per_kind = static_cast<int64_t>(total_tokens) * num_kv_heads;
+  const int64_t row =
+      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 4);
+  if (row >= 2 * rows_per_kind) return;
+  const bool is_v = row >= rows_per_kind;
+  const int64_t r = is_v ? row - rows_per_kind : row;
+  const int tok = static_cast<int>(r / num_kv_heads);
+  const int h = static_cast<int>(r % num_kv_heads);
+  const int b = find_seq(q_start, num_seqs, tok);
+  const int i = tok - q_start[b];
+  const int pos = cache_lens[b] + i;
+  const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);
+
+  const uint16_t *src = is_v ? v + b * v_ss + static_cast<int64_t>(tok) * v_st + h * v_sh
+                             : k + b * k_ss + static_cast<int64_t>(tok) * k_st + h * k_sh;
+  uint16_t *dst = (is_v ? v_pool : k_pool) + h * pool_hs + p * kHeadDim;
+  store16(dst + lane * 8, load16(src + lane * 8));
+}
+
+// ---------------------------------------------------------------------------
+// Fused q/k RMSNorm + RoPE + K/V append.
+// Row index r over [q rows | k rows | v rows], each kind token-major.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void unpack8(const u32x4 w, float (&x)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = bf16_lo(w[j]);
+    x[2 * j + 1] = bf16_hi(w[j]);
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8_rne(const float (&y)[8]) {
+  u32x4 w;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2_rne(y[2 * j], y[2 * j + 1]);
+  return w;
+}
+
+// x' = bf16((x * rsqrt(mean(x^2) + eps)) * w), fp32 arithmetic, per head row
+// held by 16 lanes x 8 elements (torch/_decomp/decompositions.py
+// _fused_rms_norm: upcast, pow 2, mean, add eps, rsqrt, mul, mul weight,
+// cast back).
+// The squares of bf16 values are exact and so is their fp64 sum, so the
+// mean is the correctly rounded one whatever the reduction order. sqrt and
+// the reciprocal are taken in fp64 and rounded to fp32, which equals the
+// correctly rounded fp32 operation (53 >= 2 * 24 + 2 makes the double
+// rounding innocuous for both), independent of fp32 sqrt/div lowering.
+__device__ __forceinline__ double row16_sum_f64(double x) {
+  x += __shfl_xor(x, 8, 16);
+  x += __shfl_xor(x, 4, 16);
+  x += __shfl_xor(x, 2, 16);
+  x += __shfl_xor(x, 1, 16);
+  return x;
+}
+
+__device__ __forceinline__ void rms_norm8(float (&x)[8],
+                                          const uint16_t *__restrict__ w,
+                                          int lane, float eps) {
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += static_cast<double>(x[j] * x[j]);
+  ss = row16_sum_f64(ss);
+  const float mean = static_cast<float>(ss) * (1.0f / kHeadDim);
+  const float root = static_cast<float>(sqrt(static_cast<double>(mean + eps)));
+  const float rstd = static_cast<float>(1.0 / static_cast<double>(root));
+  const u32x4 wv = load16(w + lane * 8);
+  float wf[8];
+  unpack8(wv, wf);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float y = (x[j] * rstd) * wf[j];
+    x[j] = bf16_to_f32(static_cast<uint16_t>(f32_to_bf16_rne(y)));
+  }
+}
+
+// y = bf16(x * cos + rotate_half(x) * sin), rotate_half(x) = cat(-x2, x1)
+// (hayate/model/rope.py:31-47). Lane l holds features 8l..8l+7; its partner
+// l ^ 8 holds the other half.
+__device__ __forceinline__ void rope8(float (&x)[8],
+                                      const float *__restrict__ cos_row,
+                                      const float *__restrict__ sin_row,
+                                      int lane) {
+  float other[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) other[j] = __shfl_xor(x[j], 8, 16);
+  const float sgn = lane < 8 ? -1.0f : 1.0f;
+  const f32x4 c0 = *reinterpret_cast<const f32x4 *>(cos_row + lane * 8);
+  const f32x4 c1 = *reinterpret_cast<const f32x4 *>(cos_row + lane * 8 + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4 *>(sin_row + lane * 8);
+  const f32x4 s1 = *reinterpret_cast<const f32x4 *>(sin_row + lane * 8 + 4);
+  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  const float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float a = x[j] * c[j];
+    const float r = (sgn * other[j]) * s[j];
+    x[j] = a + r;
+  }
+}
+
+__global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
+    const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
+    uint16_t *__restrict__ q_out, int64_t qo_ss, int64_t qo_st, int64_t qo_sh,
+    const uint16_t *__restrict__ k, int64_t k_ss, int64_t k_st, int64_t k_sh,
+    const uint16_t *__restrict__ v, int64_t v_ss, int64_t v_st, int64_t v_sh,
+    const uint16_t *__restrict__ q_w, const uint16_t *__restrict__ k_w,
+    float eps, const float *__restrict__ cos_t,
+    const float *__restrict__ sin_t, uint16_t *__restrict__ k_pool,
+    uint16_t *__restrict__ v_pool, int64_t pool_hs,
+    const int32_t *__restrict__ q_start, const int32_t *__restrict__ cache_lens,
+    const int32_t *__restrict__ page_table, int64_t pt_stride, int num_seqs,
+    int total_tokens, int num_q_heads, int num_kv_heads, int page_size) {
+  const int lane = threadIdx.x & 15;
+  const int64_t nq = static_cast<int64_t>(total_tokens) * num_q_heads;
+  const int64_t nk = static_cast<int64_t>(total_tokens) * num_kv_heads;
+  const int64_t row =
+      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 4);
+  if (row >= nq + 2 * nk) return;
+
+  int kind;  // 0 = q, 1 = k, 2 = v
+  int64_t r;
+  int heads;
+  if (row < nq) {
+    kind = 0; r = row; heads = num_q_heads;
+  } else if (row < nq + nk) {
+    kind = 1; r = row - nq; heads = num_kv_heads;
+  } else {
+    kind = 2; r = row - nq - nk; heads = num_kv_heads;
+  }
+  const int tok = static_cast<int>(r / heads);
+  const int h = static_cast<int>(r % heads);
+  const int b = find_seq(q_start, num_seqs, tok);
+  const int i = tok - q_start[b];
+  const int pos = cache_lens[b] + i;
+
+  if (kind == 2) {
+    const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);
+    const uint16_t *src = v + b * v_ss + static_cast<int64_t>(tok) * v_st + h * v_sh;
+    store16(v_pool + h * pool_hs + p * kHeadDim + lane * 8, load16(src + lane * 8));
+    return;
+  }
+
+  const uint16_t *src = kind == 0
+      ? q + b * q_ss + static_cast<int64_t>(tok) * q_st + h * q_sh
+      : k + b * k_ss + static_cast<int64_t>(tok) * k_st + h * k_sh;
+  float x[8];
+  unpack8(load16(src + lane * 8), x);
+  const uint16_t *w = kind == 0 ? q_w : k_w;
+  if (w != nullptr) rms_norm8(x, w, lane, eps);
+  if (cos_t != nullptr) {
+    const int64_t off = static_cast<int64_t>(pos) * kHeadDim;
+    rope8(x, cos_t + off, sin_t + off, lane);
+  }
+  const u32x4 y = pack8_rne(x);
+  if (kind == 0) {
+    store16(q_out + b * qo_ss + static_cast<int64_t>(tok) * qo_st + h * qo_sh + lane * 8, y);
+  } else {
+    const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);
+    store16(k_pool + h * pool_hs + p * kHeadDim + lane * 8, y);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gather / scatter between pages and a (layer, head, token) tensor.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void page_gather_kernel(
+    const uint16_t *__restrict__ pool, int64_t pool_ls, int64_t pool_hs,
+    const int32_t *__restrict__ pages, int length, uint16_t *__restrict__ out,
+    int num_layers, int num_kv_heads, int page_size) {
+  const int lane = threadIdx.x & 15;
+  const int64_t rows = static_cast<int64_t>(num_layers) * num_kv_heads * length;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 4);
+       row < rows; row += static_cast<int64_t>(gridDim.x) * kRowsPerBlock) {
+    const int t = static_cast<int>(row % length);
+    const int64_t lh = row / length;
+    const int h = static_cast<int>(lh % num_kv_heads);
+    const int l = static_cast<int>(lh / num_kv_heads);
+    const int64_t p = static_cast<int64_t>(pages[t / page_size]) * page_size + t % page_size;
+    const uint16_t *src = pool + l * pool_ls + h * pool_hs + p * kHeadDim;
+    store16(out + row * kHeadDim + lane * 8, load16(src + lane * 8));
+  }
+}
+
+__global__ __launch_bounds__(256) void page_scatter_kernel(
+    uint16_t *__restrict__ pool, int64_t pool_ls, int64_t pool_hs,
+    const int32_t *__restrict__ pages, int length,
+    const uint16_t *__restrict__ src, int64_t s_ls, int64_t s_hs, int64_t s_ts,
+    int num_layers, int num_kv_heads, int page_size) {
+  const int lane = threadIdx.x & 15;
+  const int64_t rows = static_cast<int64_t>(num_layers) * num_kv_heads * length;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 4);
+       row < rows; row += static_cast<int64_t>(gridDim.x) * kRowsPerBlock) {
+    const int t = static_cast<int>(row % length);
+    const int64_t lh = row / length;
+    const int h = static_cast<int>(lh % num_kv_heads);
+    const int l = static_cast<int>(lh / num_kv_heads);
+    const int64_t p = static_cast<int64_t>(pages[t / page_size]) * page_size + t % page_size;
+    uint16_t *dst = pool + l * pool_ls + h * pool_hs + p * kHeadDim;
+    store16(dst + lane * 8, load16(src + l * s_ls + h * s_hs + t * s_ts + lane * 8));
+  }
+}
+
+inline unsigned grid_for_rows(int64_t rows) {
+  return static_cast<unsigned>((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Error plumbing shared by every translation unit.
+// ---------------------------------------------------------------------------
+static thread_local char g_err[512] = "";
+
+void set_error(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+int launch_status(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return HY_ELAUNCH;
+  }
+  return HY_OK;
+}
+
+const char *last_error() { return g_err; }
+
+}  // namespace hy
+
+using hy::kHeadDim;
+
+extern "C" int hy_version(void) { return (0 << 16) | 1; }
+
+extern "C" const char *hy_last_error(void) { return hy::last_error(); }
+
+static int check_common(int32_t num_seqs, int32_t total_tokens,
+                        int32_t num_kv_heads, int32_t head_dim,
+                        int32_t page_size) {
+  HY_REQUIRE(num_seqs >= 1, "num_seqs must be positive (got %d)", num_seqs);
+  HY_REQUIRE(total_tokens >= 0, "total_tokens must be non-negative");
+  HY_REQUIRE(num_kv_heads >= 1, "num_kv_heads must be positive");
+  HY_REQUIRE_SUPPORTED(head_dim == kHeadDim,
+                       "head_dim %d unsupported (kernels are built for %d)",
+                       head_dim, kHeadDim);
+  HY_REQUIRE_SUPPORTED(page_size >= 32 && page_size % 32 == 0,
+                       "page_size %d unsupported (multiple of 32 required)",
+                       page_size);
+  return HY_OK;
+}
+
+extern "C" int hy_kv_append(void *k_pool, void *v_pool,
+                            int64_t pool_head_stride, const void *k,
+                            int64_t k_stride_seq, int64_t k_stride_tok,
+                            int64_t k_stride_head, const void *v,
+                            int64_t v_stride_seq, int64_t v_stride_tok,
+                            int64_t v_stride_head, const int32_t *q_start,
+                            const int32_t *cache_lens,
+                            const int32_t *page_table,
+                            int64_t page_table_stride, int32_t num_seqs,
+                            int32_t total_tokens, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t page_size,
+                            void *stream) {
+  hy::clear_error();
+  if (int rc = check_common(num_seqs, total_tokens, num_kv_heads, head_dim, page_size))
+    return rc;
+  HY_REQUIRE(k_pool && v_pool && k && v && q_start && cache_lens && page_table,
+             "hy_kv_append: null pointer argument");
+  if (total_tokens == 0) return HY_OK;
+  const int64_t rows = 2LL * total_tokens * num_kv_heads;
+  hipLaunchKernelGGL(hy::kv_append_kernel, dim3(hy::grid_for_rows(rows)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<uint16_t *>(k_pool),
+                     static_cast<uint16_t *>(v_pool), pool_head_stride,
+                     static_cast<const uint16_t *>(k), k_stride_seq,
+                     k_stride_tok, k_stride_head,
+                     static_cast<const uint16_t *>(v), v_stride_seq,
+                     v_stride_tok, v_stride_head, q_start, cache_lens,
+                     page_table, page_table_stride, num_seqs, total_tokens,
+                     num_kv_heads, page_size);
+  return hy::launch_status("hy_kv_append");
+}
+
+extern "C" int hy_qknorm_rope_append(
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
+    int64_t q_stride_head, void *q_out, int64_t qo_stride_seq,
+    int64_t qo_stride_tok, int64_t qo_stride_head, const void *k,
+    int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
+    const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
+    int64_t v_stride_head, const void *q_norm_weight,
+    const void *k_norm_weight, float eps, const float *cos_table,
+    const float *sin_table, int32_t max_positions, void *k_pool, void *v_pool,
+    int64_t pool_head_stride, const int32_t *q_start,
+    const int32_t *cache_lens, const int32_t *page_table,
+    int64_t page_table_stride, int32_t num_seqs, int32_t total_tokens,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t page_size, void *stream) {
+  hy::clear_error();
+  if (int rc = check_common(num_seqs, total_tokens, num_kv_heads, head_dim, page_size))
+    return rc;
+  HY_REQUIRE(num_q_heads >= 1, "num_q_heads must be positive");
+  HY_REQUIRE(q && q_out && k && v && k_pool && v_pool && q_start &&
+                 cache_lens && page_table,
+             "hy_qknorm_rope_append: null pointer argument");
+  HY_REQUIRE((cos_table == nullptr) == (sin_table == nullptr),
+             "cos_table and sin_table must both be given or both be NULL");
+  HY_REQUIRE(cos_table == nullptr || max_positions > 0,
+             "max_positions must be positive when tables are given");
+  if (total_tokens == 0) return HY_OK;
+  const int64_t rows = static_cast<int64_t>(total_tokens) * (num_q_heads + 2 * num_kv_heads);
+  hipLaunchKernelGGL(
+      hy::qknorm_rope_append_kernel, dim3(hy::grid_for_rows(rows)), dim3(256),
+      0, static_cast<hipStream_t>(stream), static_cast<const uint16_t *>(q),
+      q_stride_seq, q_stride_tok, q_stride_head, static_cast<uint16_t *>(q_out),
+      qo_stride_seq, qo_stride_tok, qo_stride_head,
+      static_cast<const uint16_t *>(k), k_stride_seq, k_stride_tok,
+      k_stride_head, static_cast<const uint16_t *>(v), v_stride_seq,
+      v_stride_tok, v_stride_head,
+      static_cast<const uint16_t *>(q_norm_weight),
+      static_cast<const uint16_t *>(k_norm_weight), eps, cos_table, sin_table,
+      static_cast<uint16_t *>(k_pool), static_cast<uint16_t *>(v_pool),
+      pool_head_stride, q_start, cache_lens, page_table, page_table_stride,
+      num_seqs, total_tokens, num_q_heads, num_kv_heads, page_size);
+  return hy::launch_status("hy_qknorm_rope_append");
+}
+
+extern "C" int hy_page_gather(const void *pool, int64_t pool_layer_stride,
+                              int64_t pool_head_stride, const int32_t *pages,
+                              int32_t length, void *out, int32_t num_layers,
+                              int32_t num_kv_heads, int32_t head_dim,
+                              int32_t page_size, void *stream) {
+  hy::clear_error();
+  if (int rc = check_common(1, 0, num_kv_heads, head_dim, page_size)) return rc;
+  HY_REQUIRE(length >= 0, "length must be non-negative");
+  HY_REQUIRE(num_layers >= 1, "num_layers must be positive");
+  if (length == 0) return HY_OK;
+  HY_REQUIRE(pool && pages && out, "hy_page_gather: null pointer argument");
+  const int64_t rows = static_cast<int64_t>(num_layers) * num_kv_heads * length;
+  const int64_t blocks = (rows + 15) / 16;
+  const unsigned grid = static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
+  hipLaunchKernelGGL(hy::page_gather_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t *>(pool), pool_layer_stride,
+                     pool_head_stride, pages, length,
+                     static_cast<uint16_t *>(out), num_layers, num_kv_heads,
+                     page_size);
+  return hy::launch_status("hy_page_gather");
+}
+
+extern "C" int hy_page_scatter(void *pool, int64_t pool_layer_stride,
+                               int64_t pool_head_stride, const int32_t *pages,
+                               int32_t length, const void *src,
+                               int64_t src_stride_layer,
+                               int64_t src_stride_head, int64_t src_stride_tok,
+                               int32_t num_layers, int32_t num_kv_heads,
+                               int32_t head_dim, int32_t page_size,
+                               void *stream) {
+  hy::clear_error();
+  if (int rc = check_common(1, 0, num_kv_heads, head_dim, page_size)) return rc;
+  HY_REQUIRE(length >= 0, "length must be non-negative");
+  HY_REQUIRE(num_layers >= 1, "num_layers must be positive");
+  if (length == 0) return HY_OK;
+  HY_REQUIRE(pool && pages && src, "hy_page_scatter: null pointer argument");
+  const int64_t rows = static_cast<int64_t>(num_layers) * num_kv_heads * length;
+  const int64_t blocks = (rows + 15) / 16;
+  const unsigned grid = static_cast<unsigned>(blocks < 65536 ? blocks : 65536);
+  hipLaunchKernelGGL(hy::page_scatter_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream),
+                     static_cast<uint16_t *>(pool), pool_layer_stride,
+                     pool_head_stride, pages, length,
+                     static_cast<const uint16_t *>(src), src_stride_layer,
+                     src_stride_head, src_stride_tok, num_layers,
+                     num_kv_heads, page_size);
+  return hy::launch_status("hy_page_scatter");
+}

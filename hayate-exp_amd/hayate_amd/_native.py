@@ -1,0 +1,169 @@
+"""ctypes binding of libhayate_attn.so (the C ABI in include/hayate_attn.h).
+
+The shared library is the only compute path: if it is missing this module
+raises instead of substituting anything else. Host-only entry points
+(hy_plan_tick, hy_decode_workspace_bytes, hy_version) work without a GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+LIB_NAME = "libhayate_attn.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+HY_OK = 0
+HY_EINVAL = -1
+HY_ELAUNCH = -2
+HY_EUNSUPPORTED = -3
+HY_ENOSPACE = -4
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F32 = ctypes.c_float
+
+# Argument signatures, in header order.
+_SIGNATURES = {
+    "hy_version": ([], ctypes.c_int),
+    "hy_last_error": ([], ctypes.c_char_p),
+    "hy_kv_append": (
+        [_P, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P,
+         _I64, _I32, _I32, _I32, _I32, _I32, _P],
+        ctypes.c_int,
+    ),
+    "hy_qknorm_rope_append": (
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P,
+         _I64, _I64, _I64, _P, _P, _F32, _P, _P, _I32, _P, _P, _I64, _P, _P,
+         _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P],
+        ctypes.c_int,
+    ),
+    "hy_page_gather": (
+        [_P, _I64, _I64, _P, _I32, _P, _I32, _I32, _I32, _I32, _P],
+        ctypes.c_int,
+    ),
+    "hy_page_scatter": (
+        [_P, _I64, _I64, _P, _I32, _P, _I64, _I64, _I64, _I32, _I32, _I32,
+         _I32, _P],
+        ctypes.c_int,
+    ),
+    "hy_plan_tick": (
+        [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _I32, _P],
+        ctypes.c_int,
+    ),
+    "hy_decode_workspace_bytes": ([_I32, _I32, _I32, _I32, _I32], ctypes.c_int64),
+    "hy_paged_decode": (
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64,
+         _P, _P, _I32, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32,
+         _F32, _P],
+        ctypes.c_int,
+    ),
+    "hy_paged_prefill": (
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64,
+         _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P],
+        ctypes.c_int,
+    ),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    """The HIP library has not been built; there is no other compute path."""
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the native library, or raise loudly."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise NativeLibraryMissing(
+            f"{LIB_PATH} is not built; run `make -C hayate-exp_amd/csrc` "
+            "(or __graft_entry__.build()) first"
+        )
+    handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+    for name, (argtypes, restype) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    _lib = handle
+    return handle
+
+
+def last_error() -> str:
+    msg = lib().hy_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Map a C return code onto the exception types the reference raises."""
+    if rc == HY_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc == HY_EINVAL:
+        raise ValueError(msg)
+    if rc == HY_EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    if rc == HY_ENOSPACE:
+        raise MemoryError(msg)
+    raise RuntimeError(msg)
+
+
+class TickPlan:
+    """Host copy of one tick's work lists (hy_plan_tick)."""
+
+    __slots__ = ("decode", "prefill", "n_groups", "n_slots")
+
+    def __init__(self, decode, prefill, n_groups, n_slots):
+        self.decode = decode      # int32 (n, 8)
+        self.prefill = prefill    # int32 (n, 4)
+        self.n_groups = n_groups
+        self.n_slots = n_slots
+
+
+def plan_tick(
+    q_lens: np.ndarray,
+    kv_lens: np.ndarray,
+    num_q_heads: int,
+    num_kv_heads: int,
+    page_size: int,
+    num_cus: int,
+    tokens_per_split: int = 0,
+) -> TickPlan:
+    """Run the native tick planner.
+
+    decode rows: {seq, tok_begin, tok_end, slot, group, first_slot,
+    num_splits, 0}; prefill rows: {seq, q_begin, q_end, 0}.
+    """
+    q_lens = np.ascontiguousarray(q_lens, dtype=np.int32)
+    kv_lens = np.ascontiguousarray(kv_lens, dtype=np.int32)
+    n = int(q_lens.shape[0])
+    group = max(1, num_q_heads // max(1, num_kv_heads))
+    tile = max(1, 128 // group)
+    split_floor = 32 if tokens_per_split <= 0 else max(32, tokens_per_split)
+    dec_cap = int(sum(int(k) // split_floor + 1 for k, q in zip(kv_lens, q_lens) if q == 1)) + 1
+    pre_cap = int(sum((int(q) + tile - 1) // tile for q in q_lens if q > 1)) + 1
+    dec = np.zeros((dec_cap, 8), dtype=np.int32)
+    pre = np.zeros((pre_cap, 4), dtype=np.int32)
+    counts = np.zeros(4, dtype=np.int32)
+    rc = lib().hy_plan_tick(
+        q_lens.ctypes.data, kv_lens.ctypes.data, n, num_q_heads, num_kv_heads,
+        page_size, num_cus, tokens_per_split, dec.ctypes.data, dec_cap,
+        pre.ctypes.data, pre_cap, counts.ctypes.data,
+    )
+    check(rc, "hy_plan_tick")
+    nd, ng, npf, ns = (int(x) for x in counts)
+    return TickPlan(dec[:nd].copy(), pre[:npf].copy(), ng, ns)
+
+
+def decode_workspace_bytes(n_slots: int, n_groups: int, num_q_heads: int,
+                           num_kv_heads: int, head_dim: int) -> int:
+    return int(lib().hy_decode_workspace_bytes(n_slots, n_groups, num_q_heads,
+                                               num_kv_heads, head_dim))

@@ -1,0 +1,74 @@
+"""Grouped-query attention module for the paged path.
+
+Same constructor and forward signature as the reference's
+hayate/model/attention.py:17-122. In paged mode (the only mode Engine uses,
+engine.py:218-223) the projections stay torch GEMMs and everything between
+them runs in two HIP launches: the fused q/k RMSNorm + RoPE + KV append, then
+paged attention. The non-paged branch (contiguous history / varlen flash,
+attention.py:78-117) is not part of this library and raises.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+
+class GroupedQueryAttention(nn.Module):
+    def __init__(self, d_in, num_heads, num_kv_groups, head_dim, dtype=None):
+        super().__init__()
+        if num_heads % num_kv_groups:
+            raise ValueError("num_heads must be divisible by num_kv_groups")
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.num_kv_groups = num_kv_groups
+        self.q_proj = nn.Linear(d_in, num_heads * head_dim, bias=False, dtype=dtype)
+        self.k_proj = nn.Linear(d_in, num_kv_groups * head_dim, bias=False, dtype=dtype)
+        self.v_proj = nn.Linear(d_in, num_kv_groups * head_dim, bias=False, dtype=dtype)
+        self.o_proj = nn.Linear(num_heads * head_dim, d_in, bias=False, dtype=dtype)
+        self.q_norm = nn.RMSNorm(head_dim, eps=1e-6, dtype=dtype)
+        self.k_norm = nn.RMSNorm(head_dim, eps=1e-6, dtype=dtype)
+
+    def forward(
+        self,
+        x,
+        cos,
+        sin,
+        position_ids,
+        prev_k,
+        prev_v,
+        varlen_metadata=None,
+        paged_cache=None,
+        layer_idx=None,
+    ):
+        """x (B, T, d_in) -> (o_proj(context), None, None).
+
+        Positions are the batch's cache_lens + token index, which is what the
+        reference's position_ids hold in paged mode (qwen.py:89-109).
+        """
+        if paged_cache is None:
+            raise NotImplementedError(
+                "only the paged attention path is provided (pass paged_cache)"
+            )
+        B, T, _ = x.shape
+        q = self.q_proj(x).view(B, T, self.num_heads, self.head_dim)
+        k = self.k_proj(x).view(B, T, self.num_kv_groups, self.head_dim)
+        v = self.v_proj(x).view(B, T, self.num_kv_groups, self.head_dim)
+        q_norm_w = self.q_norm.weight if self.q_norm.weight is not None else None
+        k_norm_w = self.k_norm.weight if self.k_norm.weight is not None else None
+        eps = self.q_norm.eps if self.q_norm.eps is not None else torch.finfo(torch.float32).eps
+        if paged_cache.varlen:
+            # Varlen ticks carry packed tokens: x is (1, N, d_in).
+            if B != 1:
+                raise ValueError("a varlen tick expects x of shape (1, tokens, d_in)")
+            q_rot = paged_cache.norm_rope_write_layer(
+                layer_idx, q[0], k[0], v[0], q_norm_w, k_norm_w, eps, cos, sin
+            )
+            context = paged_cache.attend_layer(q_rot, layer_idx).unsqueeze(0)
+        else:
+            q_rot = paged_cache.norm_rope_write_layer(
+                layer_idx, q, k, v, q_norm_w, k_norm_w, eps, cos, sin
+            )
+            context = paged_cache.attend_layer(q_rot.transpose(1, 2), layer_idx).transpose(1, 2)
+        context = context.reshape(B, T, self.num_heads * self.head_dim)
+        return self.o_proj(context), None, None

@@ -1,0 +1,201 @@
+/*
+ * hayate_attn.h — C ABI of the MI355X (gfx950) paged-attention library
+ * libhayate_attn.so.
+ *
+ * Every entry point takes raw device pointers, element strides (int64, in
+ * elements, not bytes), int32 metadata and a hipStream_t (passed as void* so
+ * this header needs no HIP include). Nothing here allocates device memory:
+ * all buffers, including the split-K workspace, belong to the caller.
+ * Functions enqueue asynchronously on the given stream, never synchronise,
+ * and return 0 on success or a negative HY_E* code; hy_last_error() then
+ * returns a message for the calling thread.
+ *
+ * KV pool layout (one transformer layer, as in the reference's pool tensors
+ * of shape (layers, 1, kv_heads, capacity, head_dim), hayate/engine/
+ * paged_cache.py:104-109): element (h, p, d) of a layer lives at
+ *   base + h * pool_head_stride + p * head_dim + d
+ * with physical token p = page_id * page_size + offset.
+ *
+ * Query/key/value/output rows are addressed per sequence b, token i within
+ * that sequence and head h as
+ *   base + b * stride_seq + (q_start[b] + i) * stride_tok + h * stride_head
+ * so both a padded (B, H, T, D) view and a packed varlen (N, H, D) tensor
+ * can be passed without a copy. q_start has num_seqs + 1 entries
+ * (cumulative query lengths, q_start[0] == 0).
+ *
+ * Supported geometry: head_dim == 128, page_size a multiple of 32,
+ * num_q_heads / num_kv_heads in {1, 2, 4, 8, 16}; bf16 storage.
+ */
+#ifndef HAYATE_ATTN_H
+#define HAYATE_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HY_OK 0
+#define HY_EINVAL (-1)       /* invalid argument (shape, null pointer, range) */
+#define HY_ELAUNCH (-2)      /* HIP launch or runtime error */
+#define HY_EUNSUPPORTED (-3) /* geometry the kernels are not built for */
+#define HY_ENOSPACE (-4)     /* caller buffer too small */
+
+/* Library version, (major << 16) | minor. No reference counterpart. */
+int hy_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *hy_last_error(void);
+
+/*
+ * Paged KV append: pool[h, phys(b, c_b + i)] = k[b, i, h] (and v), a pure
+ * bit copy, for every sequence b < num_seqs, token i < q_len_b and kv head h.
+ * phys(b, t) = page_table[b * page_table_stride + t / page_size] * page_size
+ *              + t % page_size, c_b = cache_lens[b].
+ * Replaces PagedKVBatch.write_layer (hayate/engine/paged_cache.py:44-60).
+ */
+int hy_kv_append(void *k_pool, void *v_pool, int64_t pool_head_stride,
+                 const void *k, int64_t k_stride_seq, int64_t k_stride_tok,
+                 int64_t k_stride_head, const void *v, int64_t v_stride_seq,
+                 int64_t v_stride_tok, int64_t v_stride_head,
+                 const int32_t *q_start, const int32_t *cache_lens,
+                 const int32_t *page_table, int64_t page_table_stride,
+                 int32_t num_seqs, int32_t total_tokens, int32_t num_kv_heads,
+                 int32_t head_dim, int32_t page_size, void *stream);
+
+/*
+ * Fused per-head RMSNorm + rotary embedding of q and k, then paged append of
+ * k and v. For token i of sequence b at position pos = cache_lens[b] + i:
+ *   x' = bf16((x * (1 / sqrt(mean(x^2) + eps))) * w)          (fp32 math)
+ *   y  = bf16(x' * cos[pos] + rotate_half(x') * sin[pos])       (fp32 math)
+ * q' goes to q_out; k' and v (unchanged) are appended as hy_kv_append does.
+ * q_norm_weight / k_norm_weight may be NULL (no norm); cos_table/sin_table
+ * may be NULL (no rotation); tables are fp32 (max_positions, head_dim).
+ * Replaces GroupedQueryAttention.forward lines 62-75 (hayate/model/
+ * attention.py:62-75: q_norm, k_norm, apply_rope_vectorized, write_layer),
+ * with hayate/model/rope.py:31-47 for the rotation.
+ */
+int hy_qknorm_rope_append(
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
+    int64_t q_stride_head, void *q_out, int64_t qo_stride_seq,
+    int64_t qo_stride_tok, int64_t qo_stride_head, const void *k,
+    int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
+    const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
+    int64_t v_stride_head, const void *q_norm_weight,
+    const void *k_norm_weight, float eps, const float *cos_table,
+    const float *sin_table, int32_t max_positions, void *k_pool, void *v_pool,
+    int64_t pool_head_stride, const int32_t *q_start,
+    const int32_t *cache_lens, const int32_t *page_table,
+    int64_t page_table_stride, int32_t num_seqs, int32_t total_tokens,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t page_size, void *stream);
+
+/*
+ * Page gather: out[l, h, t, :] = pool[l, h, phys(t), :] for t < length over
+ * the given page list, out contiguous (num_layers, num_kv_heads, length,
+ * head_dim). A bit copy. Replaces PagedKVCacheManager.snapshot's
+ * index_select (hayate/engine/paged_cache.py:180-190, 306-315).
+ */
+int hy_page_gather(const void *pool, int64_t pool_layer_stride,
+                   int64_t pool_head_stride, const int32_t *pages,
+                   int32_t length, void *out, int32_t num_layers,
+                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                   void *stream);
+
+/*
+ * Page scatter, the inverse of hy_page_gather: pool[l, h, phys(t), :] =
+ * src[l, h, t, :] with src strided (layer, head, token). Replaces
+ * PagedKVCacheManager.import_cache's index_copy_ (paged_cache.py:153-166).
+ */
+int hy_page_scatter(void *pool, int64_t pool_layer_stride,
+                    int64_t pool_head_stride, const int32_t *pages,
+                    int32_t length, const void *src, int64_t src_stride_layer,
+                    int64_t src_stride_head, int64_t src_stride_tok,
+                    int32_t num_layers, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t page_size, void *stream);
+
+/*
+ * Tick planner (host only, no device access). Given per-sequence query
+ * lengths and KV lengths (kv_len = cache_len + q_len), split the work of
+ * one attention call into:
+ *   decode items  (q_len == 1): int32[n][8] =
+ *                 {seq, tok_begin, tok_end, slot, group, first_slot,
+ *                  num_splits, 0}
+ *                 tok_begin is a multiple of 32; a sequence with one split
+ *                 has slot = group = -1 and writes its output directly;
+ *                 otherwise its splits own workspace slots first_slot ..
+ *                 first_slot + num_splits - 1 and share merge group `group`;
+ *   prefill items (q_len > 1):  int32[n][4] = {seq, q_begin, q_end, 0}
+ *                 query tiles of the sequence, most keys first.
+ * counts_out receives {n_decode, n_groups, n_prefill, n_slots}.
+ * Capacities are in items; returns HY_ENOSPACE if one is too small.
+ * target_tokens_per_split sets the decode split length (rounded up to a
+ * multiple of 32); <= 0 picks one from the total decode work and num_cus.
+ * Replaces the per-forward metadata of PagedKVCacheManager.begin_batch
+ * (paged_cache.py:202-293: page table, cache_lens, kv_lens, block mask).
+ */
+int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
+                 int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+                 int32_t page_size, int32_t num_cus,
+                 int32_t target_tokens_per_split, int32_t *decode_items,
+                 int32_t decode_capacity, int32_t *prefill_items,
+                 int32_t prefill_capacity, int32_t *counts_out);
+
+/*
+ * Split-K workspace bytes: n_slots fp32 partials (acc[head_dim], max, sum
+ * per query head) plus one int32 arrival counter per (group, kv head).
+ * The counters must be zero before the first call; every call leaves them
+ * zero again.
+ */
+int64_t hy_decode_workspace_bytes(int32_t n_slots, int32_t n_groups,
+                                  int32_t num_q_heads, int32_t num_kv_heads,
+                                  int32_t head_dim);
+
+/*
+ * Paged GQA decode attention for sequences with one query token each
+ * (items from hy_plan_tick), one kernel launch. Each workgroup covers one
+ * decode item and one kv head, loads every K/V row of its token range once
+ * and applies it to all num_q_heads / num_kv_heads query heads; for a
+ * sequence with several splits, the workgroup that finishes last merges the
+ * fp32 partials of all splits (log-sum-exp) and writes the output.
+ * Causal semantics: query i of sequence b sees logical keys
+ * k <= cache_len_b + i with kv_len = cache_len + 1 (paged_cache.py:266-271).
+ * Calls that share a workspace must not overlap in time.
+ * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T == 1.
+ */
+int hy_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
+                    int64_t q_stride_head, void *out, int64_t o_stride_seq,
+                    int64_t o_stride_tok, int64_t o_stride_head,
+                    const void *k_pool, const void *v_pool,
+                    int64_t pool_head_stride, const int32_t *page_table,
+                    int64_t page_table_stride, const int32_t *q_start,
+                    const int32_t *decode_items, int32_t n_decode,
+                    int32_t n_groups, int32_t n_slots, void *workspace,
+                    int64_t workspace_bytes, int32_t num_seqs,
+                    int32_t num_q_heads, int32_t num_kv_heads,
+                    int32_t head_dim, int32_t page_size, float scale,
+                    void *stream);
+
+/*
+ * Paged chunked-prefill causal attention (bf16 MFMA) for sequences with
+ * q_len > 1 (prefill items from hy_plan_tick): query i of sequence b at
+ * logical position cache_lens[b] + i sees every cached prefix key and the
+ * chunk's keys up to itself. K/V are read through the page table.
+ * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T > 1.
+ */
+int hy_paged_prefill(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
+                     int64_t q_stride_head, void *out, int64_t o_stride_seq,
+                     int64_t o_stride_tok, int64_t o_stride_head,
+                     const void *k_pool, const void *v_pool,
+                     int64_t pool_head_stride, const int32_t *page_table,
+                     int64_t page_table_stride, const int32_t *q_start,
+                     const int32_t *kv_lens, const int32_t *prefill_items,
+                     int32_t n_prefill, int32_t num_seqs, int32_t num_q_heads,
+                     int32_t num_kv_heads, int32_t head_dim,
+                     int32_t page_size, float scale, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HAYATE_ATTN_H */

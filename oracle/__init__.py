@@ -1,0 +1,5 @@
+"""Oracle: CPU restatement of the reference's paged-attention path.
+
+TEST INFRASTRUCTURE ONLY — imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package.
+"""

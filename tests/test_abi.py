@@ -1,0 +1,132 @@
+"""The C ABI without a GPU: the library loads, exports every function the
+header declares, the host-only planner behaves, and argument validation
+returns error codes before any device work."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from hayate_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hayate_attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(hy_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _native.lib()
+    names = declared_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_native.EXPORTED_SYMBOLS)
+    assert lib.hy_version() >= 1
+
+
+def test_symbols_are_plain_c_in_the_dynamic_table():
+    out = os.popen(f"nm -D --defined-only {_native.LIB_PATH}").read()
+    for name in declared_functions():
+        assert re.search(rf"\bT {name}$", out, re.M), name
+
+
+def plan(q, kv, hq=32, hkv=8, page=128, cus=256, split=0):
+    return _native.plan_tick(np.array(q), np.array(kv), hq, hkv, page, cus, split)
+
+
+@pytest.mark.parametrize("split", [0, 96, 256, 1000])
+def test_plan_decode_covers_every_token_once(split):
+    rng = np.random.default_rng(0)
+    kv = rng.integers(1, 9000, size=40)
+    p = plan([1] * 40, kv, split=split)
+    dec = p.decode
+    assert len(p.prefill) == 0
+    groups = set()
+    for b in range(40):
+        items = dec[dec[:, 0] == b]
+        assert items[0, 1] == 0 and items[-1, 2] == kv[b]
+        assert (items[1:, 1] == items[:-1, 2]).all()
+        assert (items[:, 1] % 32 == 0).all() and (items[:, 2] > items[:, 1]).all()
+        assert (items[:, 6] == len(items)).all()
+        if len(items) == 1:
+            assert items[0, 3] == -1 and items[0, 4] == -1
+        else:
+            first = items[0, 5]
+            assert (items[:, 3] == np.arange(first, first + len(items))).all()
+            assert len(set(items[:, 4])) == 1
+            groups.add(int(items[0, 4]))
+    assert groups == set(range(p.n_groups))
+    assert p.n_slots == int((dec[:, 3] >= 0).sum())
+
+
+def test_plan_splits_are_balanced():
+    p = plan([1], [300], split=256)
+    assert [tuple(r[1:3]) for r in p.decode] == [(0, 160), (160, 300)]
+
+
+def test_plan_prefill_tiles_longest_first():
+    p = plan([512, 512, 1, 3], [512, 4096, 700, 10])
+    dec, pre = p.decode, p.prefill
+    assert len(dec) >= 1 and (dec[:, 0] == 2).all()
+    tile = 128 // 4
+    assert len(pre) == 2 * (512 // tile) + 1
+    keys = [(4096 - 512 if s == 1 else (10 - 3 if s == 3 else 0)) + q1 for s, q0, q1, _ in pre]
+    assert keys == sorted(keys, reverse=True)
+    covered = {}
+    for s, q0, q1, _ in pre:
+        covered.setdefault(int(s), []).append((int(q0), int(q1)))
+    for s, ql in [(0, 512), (1, 512), (3, 3)]:
+        spans = sorted(covered[s])
+        assert spans[0][0] == 0 and spans[-1][1] == ql
+        assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
+
+
+def test_plan_rejects_bad_input():
+    with pytest.raises(ValueError):
+        plan([2], [1])  # kv_len < q_len
+    with pytest.raises(ValueError):
+        plan([1], [5], hq=6, hkv=4)
+    with pytest.raises(NotImplementedError):
+        plan([1], [5], page=48)
+
+
+def test_workspace_size():
+    assert _native.decode_workspace_bytes(0, 0, 32, 8, 128) == 0
+    n = _native.decode_workspace_bytes(3, 1, 32, 8, 128)
+    assert n % 256 == 0 and n >= 3 * 32 * 130 * 4 + 8 * 4
+
+
+def test_entry_points_validate_before_touching_the_device():
+    lib = _native.lib()
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    # head_dim 64 is not built
+    rc = lib.hy_kv_append(fake, fake, 0, fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, fake, 0,
+                          1, 1, 8, 64, 128, None)
+    assert rc == _native.HY_EUNSUPPORTED and "head_dim" in _native.last_error()
+    # null pointers
+    rc = lib.hy_kv_append(None, fake, 0, fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, fake, 0,
+                          1, 1, 8, 128, 128, None)
+    assert rc == _native.HY_EINVAL
+    # page size not a multiple of 32
+    rc = lib.hy_page_gather(fake, 0, 0, fake, 10, fake, 1, 8, 128, 100, None)
+    assert rc == _native.HY_EUNSUPPORTED
+    # GQA group 3 is not built
+    rc = lib.hy_paged_decode(fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, 0, fake, 0, fake,
+                             fake, 1, 0, 0, None, 0, 1, 6, 2, 128, 128, 0.1, None)
+    assert rc == _native.HY_EUNSUPPORTED
+    # workspace too small for the slots
+    rc = lib.hy_paged_decode(fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, 0, fake, 0, fake,
+                             fake, 2, 1, 2, fake, 100, 1, 32, 8, 128, 128, 0.1, None)
+    assert rc == _native.HY_ENOSPACE
+    with pytest.raises(MemoryError):
+        _native.check(rc, "hy_paged_decode")
+    # nothing to do is success, even with null buffers
+    assert lib.hy_paged_prefill(None, 0, 0, 0, None, 0, 0, 0, None, None, 0, None, 0, None,
+                                None, None, 0, 1, 32, 8, 128, 128, 0.1, None) == 0
+    assert lib.hy_last_error() == b""

@@ -1,0 +1,250 @@
+"""GPU parity of the HIP path against the oracle.
+
+* KV append and page gather/scatter: bit-exact.
+* Fused q/k RMSNorm + RoPE: bit-exact (rotated q and the appended K rows).
+* Attention output (bf16): max-abs <= 2e-2, mean-abs <= 2e-3 and
+  error-RMS / output-RMS <= 1e-2 against the float64 oracle.
+
+Covers the five workloads at full size, the reference's own paged-attention
+test scenario (tests/test_paged_cache.py:58-112: histories 130 and 200,
+query length 2, imported through import_cache), the GroupedQueryAttention
+module, split-count invariance, ragged lengths around slice and page
+boundaries, copy-on-write of shared pages and a 256-token page size.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import EPS, assert_attention_close, bits, gpu_step, layer_bits, oracle_step, say
+from oracle import paged_ref as R
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from hayate_amd import Cache, PagedKVCacheManager
+    from hayate_amd.attention import GroupedQueryAttention
+    from hayate_amd.rope import compute_rope_params
+    from hayate_amd.workloads import ORDER, make_workload
+else:  # collected on CPU only to be deselected
+    ORDER = []
+
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("name", ["decode_b1", "decode_b32", "prefill_4x512", "mixed_tick",
+                                  "decode_32k"])
+def test_workload_parity(name):
+    say(f"[workload {name}]")
+    w = make_workload(name, device=DEV)
+    pre_k, pre_v = layer_bits(w.manager)
+    q_rot, out = gpu_step(w)
+    post_k, post_v = layer_bits(w.manager)
+    pk, pv, q_exp, o_exp = oracle_step(w, pre_k, pre_v)
+    assert np.array_equal(bits(q_rot), q_exp), "rotated q differs"
+    assert np.array_equal(post_v, pv), "V pool differs (append must be a bit copy)"
+    assert np.array_equal(post_k, pk), "K pool differs (norm + rope + append)"
+    assert_attention_close(bits(out), o_exp, name)
+
+
+def test_reference_paged_test_scenario():
+    """test_paged_cache.py:58-112 at head_dim 128: histories 130 and 200
+    imported through import_cache, query length 2, write_layer then
+    attend_layer on the uniform (B, H, T, D) layout."""
+    say("[reference scenario]")
+    torch.manual_seed(23)
+    hkv, hq, d = 2, 4, 128
+    m = PagedKVCacheManager(num_layers=1, num_kv_heads=hkv, head_dim=d, max_cache_tokens=1024,
+                            page_size=128, max_requests=2, dtype=torch.bfloat16, device=DEV)
+    m.k_cache.normal_()
+    m.v_cache.normal_()
+    handles, hist_k, hist_v = [], [], []
+    for length in (130, 200):
+        k = torch.randn(1, hkv, length, d, device=DEV, dtype=torch.bfloat16)
+        v = torch.randn_like(k)
+        handles.append(m.allocate_for_request(Cache.from_tensors(k, v)))
+        hist_k.append(k)
+        hist_v.append(v)
+    state = m.begin_batch(handles, 2)
+    q = torch.randn(2, hq, 2, d, device=DEV, dtype=torch.bfloat16)
+    new_k = torch.randn(2, hkv, 2, d, device=DEV, dtype=torch.bfloat16)
+    new_v = torch.randn_like(new_k)
+    state.write_layer(0, new_k, new_v)
+    out = state.attend_layer(q, 0)
+    torch.cuda.synchronize()
+    m.commit_batch(handles, 2)
+    # the pages hold history + new rows exactly (gather is a bit copy)
+    for row, h in enumerate(handles):
+        snap = m.snapshot(h)
+        expect_k = torch.cat((hist_k[row], new_k[row : row + 1]), dim=2)
+        expect_v = torch.cat((hist_v[row], new_v[row : row + 1]), dim=2)
+        assert torch.equal(snap.k.view(torch.int16), expect_k.view(torch.int16))
+        assert torch.equal(snap.v.view(torch.int16), expect_v.view(torch.int16))
+    pk, pv = layer_bits(m)
+    q_packed = bits(q.transpose(1, 2).reshape(4, hq, d))
+    expect = R.paged_attention(q_packed, pk, pv, [h.pages for h in handles], [130, 200], [2, 2],
+                               128)
+    got = bits(out.transpose(1, 2).reshape(4, hq, d))
+    assert_attention_close(got, expect, "reference scenario")
+    # and the reference test's own check: SDPA on the logical K/V, rtol/atol 3e-2
+    for row, old in enumerate((130, 200)):
+        keys = torch.cat((hist_k[row][0], new_k[row]), dim=1).float()[None]
+        vals = torch.cat((hist_v[row][0], new_v[row]), dim=1).float()[None]
+        allowed = torch.arange(old + 2, device=DEV)[None, :] <= (old + torch.arange(2, device=DEV))[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            q[row : row + 1].float(), keys, vals, attn_mask=allowed[None, None], enable_gqa=True)
+        torch.testing.assert_close(out[row : row + 1].float(), ref, rtol=3e-2, atol=3e-2)
+
+
+def test_attention_module_paged_forward():
+    """GroupedQueryAttention (attention.py:17-122 interface) in paged mode
+    against projections + oracle + o_proj."""
+    say("[module forward]")
+    torch.manual_seed(5)
+    d_in, hq, hkv, d, T = 256, 32, 8, 128, 3
+    mod = GroupedQueryAttention(d_in, hq, hkv, d, dtype=torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        mod.q_norm.weight.copy_(1 + 0.1 * torch.randn(d))
+        mod.k_norm.weight.copy_(1 + 0.1 * torch.randn(d))
+    cos, sin = compute_rope_params(d, 1_000_000, 40_960, device=DEV)
+    m = PagedKVCacheManager(2, hkv, d, 4096, 128, 4, torch.bfloat16, DEV, num_q_heads=hq)
+    m.k_cache.normal_()
+    m.v_cache.normal_()
+    handles = []
+    for c in (0, 77, 300):
+        h = m.allocate()
+        m.reserve(h, c)
+        h.length = c
+        handles.append(h)
+    pre_k, pre_v = layer_bits(m, 1)
+    batch = m.begin_batch(handles, T)
+    x = torch.randn(3, T, d_in, device=DEV, dtype=torch.bfloat16)
+    with torch.inference_mode():
+        y, nk, nv = mod(x, cos, sin, None, None, None, paged_cache=batch, layer_idx=1)
+        qp = mod.q_proj(x).view(3, T, hq, d)
+        kp = mod.k_proj(x).view(3, T, hkv, d)
+        vp = mod.v_proj(x).view(3, T, hkv, d)
+    torch.cuda.synchronize()
+    assert nk is None and nv is None
+    pk, pv = pre_k.copy(), pre_v.copy()
+    pages = [list(h.pages) for h in handles]
+    q_rot = R.qknorm_rope_append(bits(qp.reshape(3 * T, hq, d)), bits(kp.reshape(3 * T, hkv, d)),
+                                 bits(vp.reshape(3 * T, hkv, d)), bits(mod.q_norm.weight),
+                                 bits(mod.k_norm.weight), EPS, cos.cpu().numpy(),
+                                 sin.cpu().numpy(), pk, pv, pages, [0, 77, 300], [T] * 3, 128)
+    post_k, post_v = layer_bits(m, 1)
+    assert np.array_equal(post_k, pk) and np.array_equal(post_v, pv)
+    ctx = R.paged_attention(q_rot, pk, pv, pages, [0, 77, 300], [T] * 3, 128)
+    ctx_t = torch.from_numpy(ctx.astype(np.float32)).to(DEV).to(torch.bfloat16).reshape(3, T, hq * d)
+    with torch.inference_mode():
+        y_ref = mod.o_proj(ctx_t)
+    err = (y.float() - y_ref.float()).abs()
+    say(f"  module max_abs={err.max().item():.3e}")
+    assert err.max().item() < 5e-2 * max(1.0, y_ref.float().abs().max().item())
+
+
+@pytest.mark.parametrize("split", [64, 512, 0])
+def test_decode_split_count_does_not_change_results(split):
+    say(f"[split {split}]")
+    w = make_workload("decode_b32", device=DEV, tokens_per_split=split)
+    pre_k, pre_v = layer_bits(w.manager)
+    _, out = gpu_step(w)
+    _, _, _, o_exp = oracle_step(w, pre_k, pre_v)
+    assert_attention_close(bits(out), o_exp, f"split {split}")
+
+
+def _ragged(cache_lens, q_lens, page_size=128, pool_tokens=32768, seed=0):
+    say(f"[ragged page={page_size} c={cache_lens} q={q_lens}]")
+    hq, hkv, d = 32, 8, 128
+    g = torch.Generator().manual_seed(seed)
+    m = PagedKVCacheManager(1, hkv, d, pool_tokens, page_size, len(q_lens), torch.bfloat16, DEV,
+                            num_q_heads=hq)
+    m.k_cache.normal_()
+    m.v_cache.normal_()
+    perm = torch.randperm(m.num_pages, generator=g).tolist()
+    handles, cur = [], 0
+    for c, q in zip(cache_lens, q_lens):
+        h = m.allocate()
+        n = math.ceil((c + q) / page_size)
+        m.claim_pages(h, perm[cur : cur + n])
+        cur += n
+        h.length = c
+        handles.append(h)
+    n_tok = sum(q_lens)
+    q = torch.randn(n_tok, hq, d, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(n_tok, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(n_tok, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    pre_k, pre_v = layer_bits(m)
+    batch = m.begin_tick(handles, q_lens)
+    batch.write_layer(0, k, v)
+    out = batch.attend_layer(q, 0)
+    torch.cuda.synchronize()
+    pk, pv = pre_k.copy(), pre_v.copy()
+    pages = [list(h.pages) for h in handles]
+    R.kv_append(pk, pv, bits(k), bits(v), pages, cache_lens, q_lens, page_size)
+    post_k, post_v = layer_bits(m)
+    assert np.array_equal(post_k, pk) and np.array_equal(post_v, pv)
+    expect = R.paged_attention(bits(q), pk, pv, pages, cache_lens, q_lens, page_size)
+    assert_attention_close(bits(out), expect, "ragged")
+
+
+def test_decode_lengths_around_slice_and_page_edges():
+    ctx = [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 4095, 4096, 4097]
+    _ragged([c - 1 for c in ctx], [1] * len(ctx))
+
+
+def test_prefill_unaligned_offsets_and_short_chunks():
+    _ragged([0, 95, 1000, 128, 3], [2, 33, 100, 512, 61])
+
+
+def test_mixed_tick_small():
+    _ragged([0, 700, 5, 1023, 64], [300, 1, 1, 40, 1])
+
+
+def test_page_size_256():
+    _ragged([300, 0, 1000], [1, 70, 1], page_size=256)
+
+
+def test_copy_on_write_keeps_shared_pages_intact():
+    say("[copy on write]")
+    hq, hkv, d = 32, 8, 128
+    m = PagedKVCacheManager(1, hkv, d, 4096, 128, 3, torch.bfloat16, DEV, num_q_heads=hq)
+    m.k_cache.normal_()
+    m.v_cache.normal_()
+    parent = m.allocate()
+    m.reserve(parent, 256)
+    parent.length = 256
+    child = m.fork(parent, 256)
+    m.truncate(child, 200)  # next append lands in the shared second page
+    shared_page = parent.pages[1]
+    before = bits(m.k_cache[0, 0, :, shared_page * 128 : (shared_page + 1) * 128]).copy()
+    batch = m.begin_batch([child], 1)
+    assert child.pages[1] != shared_page and m.page_refcount(shared_page) == 1
+    k = torch.randn(1, hkv, 1, d, device=DEV, dtype=torch.bfloat16)
+    batch.write_layer(0, k, k)
+    torch.cuda.synchronize()
+    after = bits(m.k_cache[0, 0, :, shared_page * 128 : (shared_page + 1) * 128])
+    assert np.array_equal(before, after)
+    new_page = child.pages[1]
+    copy = bits(m.k_cache[0, 0, :, new_page * 128 : (new_page + 1) * 128])
+    assert np.array_equal(copy[:, :72], before[:, :72])
+    assert np.array_equal(copy[:, 72], bits(k[0, :, 0]))
+
+
+def test_gather_scatter_round_trip_bit_exact():
+    say("[gather/scatter]")
+    m = PagedKVCacheManager(3, 8, 128, 8192, 128, 2, torch.bfloat16, DEV)
+    m.k_cache.normal_()
+    m.v_cache.normal_()
+    src_k = torch.randn(3, 8, 700, 128, device=DEV, dtype=torch.bfloat16)
+    src_v = torch.randn_like(src_k)
+    h = m.allocate_for_request(Cache.from_tensors(src_k, src_v))
+    snap = m.snapshot(h, 650)
+    torch.cuda.synchronize()
+    assert torch.equal(snap.k.view(torch.int16), src_k[:, :, :650].view(torch.int16))
+    assert torch.equal(snap.v.view(torch.int16), src_v[:, :, :650].view(torch.int16))
+    # against the oracle's gather over the same pool
+    pool = bits(m.k_cache[:, 0])
+    assert np.array_equal(bits(snap.k), R.page_gather(pool, h.pages, 650, 128))
