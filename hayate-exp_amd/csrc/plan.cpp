@@ -4,17 +4,20 @@
 // Decode sequences (q_len == 1) are cut into token ranges ("splits") of equal
 // size so that every workgroup streams about the same number of K/V bytes,
 // whatever the spread of context lengths; a sequence with more than one
-// split gets consecutive workspace slots and one merge group: the last of
-// its workgroups to finish merges the partials inside the decode kernel.
-// Prefill sequences (q_len > 1) are cut into query tiles of 128 / G tokens;
-// tiles are ordered by the number of keys they read, longest first, so the
-// short tiles fill in behind the long ones.
+// split gets consecutive workspace slots and one merge item for the merge
+// pass. Ranges are listed longest first.
+// Prefill sequences (q_len > 1) are cut into query tiles of 256 / G tokens;
+// the longest tiles are split along their key range when the simulated
+// dispatch says so, and work is ordered longest first so the short items
+// fill in behind the long ones.
 
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
 
 #include <algorithm>
+#include <functional>
+#include <queue>
 #include <vector>
 
 #include "../../include/hayate_attn.h"
@@ -26,10 +29,74 @@ void clear_error();
 
 namespace {
 
-constexpr int kSlice = 32;  // decode kernel's token slice
-constexpr int kPrefillRows = 128;
+constexpr int kSlice = 32;        // decode kernel's token slice
+constexpr int kPrefillRows = 256;  // (token, head) rows of a prefill workgroup
+constexpr int kPrefillKeys = 64;   // keys per prefill step
+// Merge traffic of one prefill split partial (write + read of 256 rows of
+// fp32 O), in units of one prefill step of one workgroup.
+constexpr double kPartialCost = 0.05;
+constexpr int kDecodeWgPerCu = 2;    // decode kernel occupancy (registers)
+constexpr int64_t kWgOverhead = 96;  // fixed cost of a workgroup, in tokens
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Length of each split of a kv_len-token context cut at about `split`.
+int64_t split_len(int64_t kv, int64_t split) {
+  const int64_t nsplit = (kv + split - 1) / split;
+  return round_up((kv + nsplit - 1) / nsplit, kSlice);
+}
+
+// Makespan of the decode grid when splits of about `split` tokens are
+// dispatched longest first onto `slots` workgroup slots, each kv head a
+// separate workgroup (cost model: tokens + fixed overhead).
+int64_t decode_makespan(const std::vector<int64_t> &kvs, int64_t split, int num_kv_heads,
+                        int64_t slots) {
+  std::vector<int64_t> costs;
+  for (int64_t kv : kvs) {
+    const int64_t len = split_len(kv, split);
+    for (int64_t t = 0; t < kv; t += len)
+      costs.push_back(std::min(len, kv - t) + kWgOverhead);
+  }
+  std::sort(costs.begin(), costs.end(), std::greater<int64_t>());
+  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> free_at;
+  for (int64_t i = 0; i < slots; ++i) free_at.push(0);
+  int64_t makespan = 0;
+  for (int64_t c : costs)
+    for (int h = 0; h < num_kv_heads; ++h) {
+      const int64_t t = free_at.top() + c;
+      free_at.pop();
+      free_at.push(t);
+      makespan = std::max(makespan, t);
+    }
+  return makespan;
+}
+
+// Makespan (in steps) of prefill tiles cut into key ranges of at most
+// `max_steps` steps, dispatched longest first onto `slots` CUs, plus the
+// merge traffic of the partials they create.
+double prefill_cost(const std::vector<int64_t> &tile_steps, int64_t max_steps, int num_kv_heads,
+                    int64_t slots) {
+  std::vector<int64_t> costs;
+  int64_t partials = 0;
+  for (int64_t st : tile_steps) {
+    const int64_t n = (st + max_steps - 1) / max_steps;
+    const int64_t per = (st + n - 1) / n;
+    for (int64_t a = 0; a < st; a += per) costs.push_back(std::min(per, st - a) + 1);
+    if (n > 1) partials += n;
+  }
+  std::sort(costs.begin(), costs.end(), std::greater<int64_t>());
+  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> free_at;
+  for (int64_t i = 0; i < slots; ++i) free_at.push(0);
+  int64_t makespan = 0;
+  for (int64_t c : costs)
+    for (int h = 0; h < num_kv_heads; ++h) {
+      const int64_t t = free_at.top() + c;
+      free_at.pop();
+      free_at.push(t);
+      makespan = std::max(makespan, t);
+    }
+  return static_cast<double>(makespan) + kPartialCost * partials * num_kv_heads;
+}
 
 }  // namespace
 
@@ -38,7 +105,9 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
                             int32_t num_kv_heads, int32_t page_size,
                             int32_t num_cus, int32_t target_tokens_per_split,
                             int32_t *decode_items, int32_t decode_capacity,
+                            int32_t *merge_items, int32_t merge_capacity,
                             int32_t *prefill_items, int32_t prefill_capacity,
+                            int32_t *prefill_merge_items, int32_t prefill_merge_capacity,
                             int32_t *counts_out) {
   hy::clear_error();
   if (num_seqs < 0 || (num_seqs > 0 && (q_lens == nullptr || kv_lens == nullptr)) ||
@@ -51,8 +120,8 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
                   num_q_heads, num_kv_heads);
     return HY_EINVAL;
   }
-  if (page_size < kSlice || page_size % kSlice) {
-    hy::set_error("hy_plan_tick: page_size %d must be a multiple of %d", page_size, kSlice);
+  if (page_size < kSlice || (page_size & (page_size - 1))) {
+    hy::set_error("hy_plan_tick: page_size %d must be a power of two >= %d", page_size, kSlice);
     return HY_EUNSUPPORTED;
   }
   const int G = num_q_heads / num_kv_heads;
@@ -70,79 +139,171 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
     if (q_lens[b] == 1) decode_tokens += kv_lens[b];
   }
 
-  // Split length: about four workgroups per CU across all kv heads, in whole
-  // 128-token units, at least 256 tokens so that each wave keeps two slices.
+  // Split length: the candidate (a multiple of 128 tokens, at least 256 so
+  // that each wave keeps two slices) whose longest-first dispatch onto the
+  // GPU's workgroup slots finishes first; ties go to fewer splits.
   int64_t split = target_tokens_per_split;
   if (split <= 0) {
-    const int64_t cus = num_cus > 0 ? num_cus : 256;
-    const int64_t want = (decode_tokens * num_kv_heads + 4 * cus - 1) / (4 * cus);
-    split = std::max<int64_t>(256, round_up(std::max<int64_t>(want, 1), 128));
+    std::vector<int64_t> kvs;
+    int64_t max_kv = 0;
+    for (int b = 0; b < num_seqs; ++b)
+      if (q_lens[b] == 1) {
+        kvs.push_back(kv_lens[b]);
+        max_kv = std::max<int64_t>(max_kv, kv_lens[b]);
+      }
+    const int64_t slots = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * kDecodeWgPerCu;
+    split = std::max<int64_t>(256, round_up(std::max<int64_t>(max_kv, 1), 128));
+    int64_t best = kvs.empty() ? 0 : decode_makespan(kvs, split, num_kv_heads, slots);
+    // At most 16 candidates between 256 and the longest context.
+    const int64_t step = std::max<int64_t>(128, round_up((split - 256) / 16, 128));
+    for (int64_t cand = split - step; cand >= 256 && !kvs.empty(); cand -= step) {
+      const int64_t t = decode_makespan(kvs, cand, num_kv_heads, slots);
+      if (t < best) {
+        best = t;
+        split = cand;
+      }
+    }
   } else {
     split = round_up(split, kSlice);
   }
 
-  int32_t n_dec = 0, n_groups = 0, n_pre = 0, n_slots = 0;
+  struct Split {
+    int32_t seq, t0, t1, slot;
+  };
+  std::vector<Split> splits;
+  int32_t n_merge = 0, n_pre = 0, n_slots = 0;
   for (int b = 0; b < num_seqs; ++b) {
     if (q_lens[b] != 1) continue;
     const int64_t kv = kv_lens[b];
     // Equal-length splits (a multiple of 32 each) instead of a short tail.
-    int64_t nsplit = (kv + split - 1) / split;
-    const int64_t len = round_up((kv + nsplit - 1) / nsplit, kSlice);
-    nsplit = (kv + len - 1) / len;
+    const int64_t len = split_len(kv, split);
+    const int64_t nsplit = (kv + len - 1) / len;
     const bool merged = nsplit > 1;
-    if (n_dec + nsplit > decode_capacity) {
-      hy::set_error("hy_plan_tick: decode capacity %d too small", decode_capacity);
-      return HY_ENOSPACE;
-    }
-    for (int64_t s = 0; s < nsplit; ++s) {
-      int32_t *it = decode_items + 8 * n_dec++;
-      it[0] = b;
-      it[1] = static_cast<int32_t>(s * len);
-      it[2] = static_cast<int32_t>(std::min<int64_t>(kv, (s + 1) * len));
-      it[3] = merged ? n_slots + static_cast<int32_t>(s) : -1;
-      it[4] = merged ? n_groups : -1;
-      it[5] = merged ? n_slots : -1;
-      it[6] = static_cast<int32_t>(nsplit);
-      it[7] = 0;
-    }
+    for (int64_t s = 0; s < nsplit; ++s)
+      splits.push_back({b, static_cast<int32_t>(s * len),
+                        static_cast<int32_t>(std::min<int64_t>(kv, (s + 1) * len)),
+                        merged ? n_slots + static_cast<int32_t>(s) : -1});
     if (merged) {
+      if (n_merge >= merge_capacity) {
+        hy::set_error("hy_plan_tick: merge capacity %d too small", merge_capacity);
+        return HY_ENOSPACE;
+      }
+      int32_t *mt = merge_items + 4 * n_merge++;
+      mt[0] = b;
+      mt[1] = n_slots;
+      mt[2] = static_cast<int32_t>(nsplit);
+      mt[3] = 0;
       n_slots += static_cast<int32_t>(nsplit);
-      ++n_groups;
     }
   }
+  if (static_cast<int64_t>(splits.size()) > decode_capacity) {
+    hy::set_error("hy_plan_tick: decode capacity %d too small (need %zu)", decode_capacity,
+                  splits.size());
+    return HY_ENOSPACE;
+  }
+  // Longest ranges first: the workgroup dispatcher then fills in the short
+  // ones behind them.
+  std::stable_sort(splits.begin(), splits.end(), [](const Split &a, const Split &b) {
+    return a.t1 - a.t0 > b.t1 - b.t0;
+  });
+  const int32_t n_dec = static_cast<int32_t>(splits.size());
+  for (int32_t i = 0; i < n_dec; ++i) {
+    int32_t *it = decode_items + 4 * i;
+    it[0] = splits[i].seq;
+    it[1] = splits[i].t0;
+    it[2] = splits[i].t1;
+    it[3] = splits[i].slot;
+  }
 
+  // Prefill: query tiles of 256 / G tokens; the key range of a tile is
+  // [0, cache_len + q_end). The longest tiles are split into key ranges of
+  // at most max_steps 64-key steps when that shortens the simulated run.
   struct Tile {
-    int32_t seq, q0, q1;
-    int64_t keys;
+    int32_t seq, q0, q1, kv_end;
+    int64_t steps;
   };
   std::vector<Tile> tiles;
   const int tile = kPrefillRows / G;
+  int64_t max_tile_steps = 0;
   for (int b = 0; b < num_seqs; ++b) {
     const int ql = q_lens[b];
     if (ql <= 1) continue;
     const int cache = kv_lens[b] - ql;
     for (int q0 = 0; q0 < ql; q0 += tile) {
       const int q1 = std::min(ql, q0 + tile);
-      tiles.push_back({b, q0, q1, static_cast<int64_t>(cache) + q1});
+      const int64_t st = (cache + q1 + kPrefillKeys - 1) / kPrefillKeys;
+      tiles.push_back({b, q0, q1, cache + q1, st});
+      max_tile_steps = std::max(max_tile_steps, st);
     }
   }
-  std::stable_sort(tiles.begin(), tiles.end(),
-                   [](const Tile &a, const Tile &b) { return a.keys > b.keys; });
-  if (static_cast<int64_t>(tiles.size()) > prefill_capacity) {
-    hy::set_error("hy_plan_tick: prefill capacity %d too small (need %zu)",
-                  prefill_capacity, tiles.size());
+  int64_t max_steps = std::max<int64_t>(max_tile_steps, 1);
+  if (!tiles.empty()) {
+    std::vector<int64_t> tile_steps;
+    for (const Tile &t : tiles) tile_steps.push_back(t.steps);
+    const int64_t slots = num_cus > 0 ? num_cus : 256;
+    double best = prefill_cost(tile_steps, max_steps, num_kv_heads, slots);
+    const int64_t step = std::max<int64_t>(1, (max_steps - 4) / 16);
+    for (int64_t cand = max_steps - step; cand >= 4; cand -= step) {
+      const double t = prefill_cost(tile_steps, cand, num_kv_heads, slots);
+      if (t < best) {
+        best = t;
+        max_steps = cand;
+      }
+    }
+  }
+  struct PItem {
+    int32_t seq, q0, q1, kv0, kv1, slot;
+  };
+  std::vector<PItem> pitems;
+  int32_t n_pmerge = 0, n_pslots = 0;
+  for (const Tile &t : tiles) {
+    const int64_t n = (t.steps + max_steps - 1) / max_steps;
+    const int64_t per = (t.steps + n - 1) / n;
+    int64_t parts = 0;
+    for (int64_t a = 0; a < t.steps; a += per) {
+      const int32_t kv0 = static_cast<int32_t>(a * kPrefillKeys);
+      const int32_t kv1 = static_cast<int32_t>(std::min<int64_t>(t.kv_end, (a + per) * kPrefillKeys));
+      pitems.push_back({t.seq, t.q0, t.q1, kv0, kv1, n > 1 ? n_pslots + static_cast<int32_t>(parts) : -1});
+      ++parts;
+    }
+    if (n > 1) {
+      if (n_pmerge >= prefill_merge_capacity) {
+        hy::set_error("hy_plan_tick: prefill merge capacity %d too small", prefill_merge_capacity);
+        return HY_ENOSPACE;
+      }
+      int32_t *mt = prefill_merge_items + 8 * n_pmerge++;
+      mt[0] = t.seq;
+      mt[1] = t.q0;
+      mt[2] = t.q1;
+      mt[3] = n_pslots;
+      mt[4] = static_cast<int32_t>(parts);
+      mt[5] = mt[6] = mt[7] = 0;
+      n_pslots += static_cast<int32_t>(parts);
+    }
+  }
+  std::stable_sort(pitems.begin(), pitems.end(), [](const PItem &a, const PItem &b) {
+    return a.kv1 - a.kv0 > b.kv1 - b.kv0;
+  });
+  if (static_cast<int64_t>(pitems.size()) > prefill_capacity) {
+    hy::set_error("hy_plan_tick: prefill capacity %d too small (need %zu)", prefill_capacity,
+                  pitems.size());
     return HY_ENOSPACE;
   }
-  for (const Tile &t : tiles) {
-    int32_t *pt = prefill_items + 4 * n_pre++;
-    pt[0] = t.seq;
-    pt[1] = t.q0;
-    pt[2] = t.q1;
-    pt[3] = 0;
+  for (const PItem &p : pitems) {
+    int32_t *pt = prefill_items + 8 * n_pre++;
+    pt[0] = p.seq;
+    pt[1] = p.q0;
+    pt[2] = p.q1;
+    pt[3] = p.kv0;
+    pt[4] = p.kv1;
+    pt[5] = p.slot;
+    pt[6] = pt[7] = 0;
   }
   counts_out[0] = n_dec;
-  counts_out[1] = n_groups;
-  counts_out[2] = n_pre;
-  counts_out[3] = n_slots;
+  counts_out[1] = n_merge;
+  counts_out[2] = n_slots;
+  counts_out[3] = n_pre;
+  counts_out[4] = n_pmerge;
+  counts_out[5] = n_pslots;
   return HY_OK;
 }

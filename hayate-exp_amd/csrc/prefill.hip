@@ -1,25 +1,38 @@
 // Paged chunked-prefill causal attention on bf16 MFMA (gfx950).
 //
-// Grid: (prefill item, kv head). An item is a tile of 128 / G query tokens of
-// one sequence; with its G query heads that is 128 (token, head) rows, which
-// all read the same K/V (GQA). Four waves, 32 rows each (two 16-row blocks).
+// Grid: (kv head, prefill item); heads vary fastest so that the dispatcher
+// walks items in the planner's longest-first order. An item is a tile of
+// 256 / G query tokens of one sequence, with its G query heads 256
+// (token, head) rows that all read the same K/V (GQA), over the key range
+// [kv_begin, kv_end) of one split. Four waves of 64 rows (two 32-row blocks).
 //
-// Per 64-key tile the workgroup stages K (row-major, 272-byte padded rows)
-// and V transposed (Vt[dim][key], 136-byte rows) in LDS; each thread moves
-// four 16-byte rows of V and writes them back as eight 8-byte key quads.
+// v_mfma_f32_32x32x16_bf16, transposed formulation (lane l, c = l % 32,
+// h = l / 32):
+//   S^T = K Q^T   A = K (32 keys x 16 dims) from LDS (one 16-byte read per
+//                 lane, 272-byte rows: conflict-free); B = Q^T held in
+//                 registers. Lane (c, h) ends with row c's scores for keys
+//                 8 (i / 4) + 4 h + i % 4, i < 16, of the 32-key block.
+//   softmax       per row: the two lanes of a row differ only in h (xor 32).
+//   O^T += V^T P^T  B = P^T: the first (last) eight of the lane's scores
+//                 are row c's probabilities for MFMA k index 8 h + j once k
+//                 stands for key 16 kh + (j < 4 ? 4 h + j : 8 + 4 h + j - 4);
+//                 A = V^T from LDS with ds_read_b64_tr_b16 (288-byte rows,
+//                 conflict-free), which hands lane r of a 16-lane group four
+//                 consecutive keys of dim r.
+// Two row blocks per wave share every K and V operand read, halving LDS
+// traffic per flop. K/V tiles of 64 keys are double buffered in LDS; the
+// next tile is loaded into registers while the current one is computed.
+// The softmax rescales lazily: the exponent base of a row only moves when
+// its max grows by more than 2^8, so the accumulators (held in AGPRs) are
+// rarely touched by VALU.
+// Rows at or past kv_end are filled from the last valid key, so masked
+// scores never meet NaN bits of unwritten rows.
 //
-// Transposed formulation with v_mfma_f32_16x16x32_bf16 (lane l, m = l % 16,
-// g = l / 16):
-//   S^T = K Q^T  A = K (16 keys x 32 dims) from LDS, B = Q^T (32 dims x 16
-//                rows) held in registers; lane (m, g) ends with the scores of
-//                row m for keys 4g..4g+3 (+16 for the second key block).
-//   softmax      per row, lanes of one row differ only in g (xor 16 / 32).
-//   O^T += V^T P^T  B = P^T needs lane (m, g) to hold row m's probabilities
-//                for 8 keys: exactly its own 8 scores once the MFMA k index
-//                8g + j is mapped to key (j < 4 ? 4g + j : 16 + 4g + j - 4);
-//                A = V^T uses the same key map, two 8-byte LDS reads.
-// The accumulator O^T[dim 16db + 4g + i][row m] keeps each row in one lane
-// group, so rescaling by the running max is a per-lane multiply.
+// A split whose item has slot >= 0 writes an fp32 partial (unnormalised
+// O^T, row max in the exp2 domain, row sum) to the workspace;
+// prefill_merge_kernel combines the splits of a query tile afterwards.
+
+#include <type_traits>
 
 #include "hy_common.h"
 
@@ -27,24 +40,25 @@ namespace hy {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kRows = 128;       // (token, head) rows per workgroup
-constexpr int kKeys = 64;        // keys per LDS tile
-constexpr int kKStride = 136;    // u16 per K row in LDS (256 B + 16 B pad)
-constexpr int kVtStride = 68;    // u16 per Vt row in LDS (128 B + 8 B pad)
+constexpr int kRows = 256;   // (token, head) rows per workgroup
+constexpr int kKeys = 64;    // keys per LDS stage
+constexpr int kKRow = 136;   // u16 per K row in LDS (272 bytes)
+constexpr int kVRow = 144;   // u16 per V row in LDS (288 bytes)
+constexpr float kLazy = 8.0f;  // rescale threshold, exp2 domain
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-__device__ __forceinline__ bf16x8 pack_p(const f32x4 a, const f32x4 b) {
+__device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base) {
   bf16x8 r;
-  r[0] = static_cast<__bf16>(a[0]);
-  r[1] = static_cast<__bf16>(a[1]);
-  r[2] = static_cast<__bf16>(a[2]);
-  r[3] = static_cast<__bf16>(a[3]);
-  r[4] = static_cast<__bf16>(b[0]);
-  r[5] = static_cast<__bf16>(b[1]);
-  r[6] = static_cast<__bf16>(b[2]);
-  r[7] = static_cast<__bf16>(b[3]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = static_cast<__bf16>(s[base + j]);
   return r;
+}
+
+__device__ __forceinline__ s16x4 tr_read(const uint16_t *p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(const_cast<uint16_t *>(p)));
 }
 
 template <int G>
@@ -54,265 +68,381 @@ __global__ __launch_bounds__(256) void prefill_kernel(
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
     int64_t pool_hs, const int32_t *__restrict__ page_table, int64_t pt_stride,
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ kv_lens,
-    const int32_t *__restrict__ items, int page_size, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kKeys * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[kHeadDim * kVtStride];
+    const int32_t *__restrict__ items, float *__restrict__ ws_acc, float *__restrict__ ws_ml,
+    int num_kv_heads, int page_shift, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKeys * kKRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kKeys * kVRow];
 
-  const int seq = items[blockIdx.x * 4 + 0];
-  const int q_begin = items[blockIdx.x * 4 + 1];
-  const int q_end = items[blockIdx.x * 4 + 2];
-  const int kvh = blockIdx.y;
+  const int32_t *it = items + 8 * blockIdx.y;
+  const int kvh = blockIdx.x;
+  const int seq = it[0];
+  const int q_begin = it[1];
+  const int q_end = it[2];
+  const int kv_begin = it[3];
+  const int kv_end = it[4];
+  const int slot = it[5];
   const int h0 = kvh * G;
   const int qs = q_start[seq];
   const int q_len = q_start[seq + 1] - qs;
   const int cache_len = kv_lens[seq] - q_len;
-  const int kv_end = cache_len + q_end;  // keys any row of this tile may see
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int l = tid & 63;
-  const int m = l & 15;
-  const int g = l >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int c = lane & 31;
+  const int h = lane >> 5;
 
-  // Q^T operand per row block: row r = 32 * wave + 16 * rb + m.
-  bf16x8 qop[2][4];
-  int row_tok[2];  // query index within the sequence for this lane's row
+  // Q^T operand of both row blocks: row r = 64 wave + 32 rb + c.
+  bf16x8 qop[2][8];
+  int row_tok[2];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    const int r = 32 * wave + 16 * rb + m;
+    const int r = 64 * wave + 32 * rb + c;
     const int i = q_begin + r / G;
-    const int h = h0 + r % G;
     row_tok[rb] = i;
     const bool live = i < q_end;
-    const uint16_t *src = q + seq * q_ss + static_cast<int64_t>(qs + (live ? i : q_begin)) * q_st + h * q_sh;
+    const uint16_t *src = q + seq * q_ss + static_cast<int64_t>(qs + (live ? i : q_begin)) * q_st +
+                          (h0 + r % G) * q_sh;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < 8; ++kk) {
       u32x4 w = {0u, 0u, 0u, 0u};
-      if (live) w = load16(src + kk * 32 + g * 8);
+      if (live) w = load16(src + 16 * kk + 8 * h);
       qop[rb][kk] = __builtin_bit_cast(bf16x8, w);
     }
   }
 
-  f32x4 acc[2][8];
+  f32x16 acc[2][4];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int db = 0; db < 8; ++db) acc[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[rb][db][i] = 0.f;
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.f, 0.f};
 
   const uint16_t *kh = k_pool + kvh * pool_hs;
   const uint16_t *vh = v_pool + kvh * pool_hs;
   const int32_t *pt = page_table + seq * pt_stride;
-  // First key that is masked for at least one row of this tile.
-  const int diag_begin = cache_len + q_begin;
+  const int page_mask = (1 << page_shift) - 1;
+  const int diag_begin = cache_len + q_begin;  // first key masked for some row
 
-  // Staging assignment: K chunk c = tid + 256 j -> (row c / 16, col c % 16);
-  // V: thread owns dims 8 * (tid % 16) .. +7 of keys 4 * (tid / 16) .. +3.
-  const int vd = (tid & 15) * 8;
-  const int vk = (tid >> 4) * 4;
-
-  for (int kt = 0; kt < kv_end; kt += kKeys) {
-    __syncthreads();  // previous tile fully consumed
+  // Staging: thread t moves 16-byte chunks j * 256 + t of the K and V tiles
+  // (row = chunk / 16, dims 8 (chunk % 16) .. +7). A tile starts at a
+  // multiple of 64 keys, so rows 0-31 and 32-63 each lie in one page: two
+  // wave-uniform (scalar) page lookups per tile. Rows at or past kv_end
+  // read the last valid key instead (any finite data: their scores are
+  // masked), so the loads need no branch and the stores no select.
+  auto load_tile = [&](int kt, u32x4(&kr)[4], u32x4(&vr)[4]) __attribute__((always_inline)) {
+    const int last = kv_end - 1;
+    const int64_t page_lo = pt[kt >> page_shift];
+    const int64_t page_hi = pt[min(kt + 32, last) >> page_shift];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int c = tid + 256 * j;
-      const int row = c >> 4;
-      const int col = c & 15;
-      const int key = kt + row;
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (key < kv_end) {
-        const int64_t p = static_cast<int64_t>(pt[key / page_size]) * page_size + key % page_size;
-        w = load16(kh + p * kHeadDim + col * 8);
-      }
-      *reinterpret_cast<u32x4 *>(&sK[row * kKStride + col * 8]) = w;
+      const int ch = tid + 256 * j;
+      const int row = ch >> 4;
+      const int key = min(kt + row, last);
+      const int64_t p = ((row < 32 ? page_lo : page_hi) << page_shift) + (key & page_mask);
+      kr[j] = load16(kh + p * kHeadDim + (ch & 15) * 8);
+      vr[j] = load16(vh + p * kHeadDim + (ch & 15) * 8);
     }
-    {
-      u32x4 vr[4];
+  };
+  auto store_tile = [&](int b, const u32x4(&kr)[4], const u32x4(&vr)[4])
+                        __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kt + vk + i;
-        vr[i] = u32x4{0u, 0u, 0u, 0u};
-        if (key < kv_end) {
-          const int64_t p = static_cast<int64_t>(pt[key / page_size]) * page_size + key % page_size;
-          vr[i] = load16(vh + p * kHeadDim + vd);
-        }
-      }
-      // Transpose 4 keys x 8 dims into 8 dims x 4 keys.
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t lo01 = (vr[0][j] & 0xffffu) | (vr[1][j] << 16);
-        const uint32_t lo23 = (vr[2][j] & 0xffffu) | (vr[3][j] << 16);
-        const uint32_t hi01 = (vr[0][j] >> 16) | (vr[1][j] & 0xffff0000u);
-        const uint32_t hi23 = (vr[2][j] >> 16) | (vr[3][j] & 0xffff0000u);
-        uint32_t *d0 = reinterpret_cast<uint32_t *>(&sVt[(vd + 2 * j) * kVtStride + vk]);
-        uint32_t *d1 = reinterpret_cast<uint32_t *>(&sVt[(vd + 2 * j + 1) * kVtStride + vk]);
-        d0[0] = lo01;
-        d0[1] = lo23;
-        d1[0] = hi01;
-        d1[1] = hi23;
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int ch = tid + 256 * j;
+      *reinterpret_cast<u32x4 *>(&sK[b][(ch >> 4) * kKRow + (ch & 15) * 8]) = kr[j];
+      *reinterpret_cast<u32x4 *>(&sV[b][(ch >> 4) * kVRow + (ch & 15) * 8]) = vr[j];
     }
-    __syncthreads();
+  };
 
-    const bool need_mask = kt + kKeys > diag_begin;
+  // Per-lane LDS bases: K operand row c, dims 8 h; V^T transposed read: row
+  // 4 (q16 / 2) + r16 / 4 of the key quad, dims 16 (q16 % 2) + 4 (r16 % 4).
+  const int r16 = lane & 15;
+  const int q16 = lane >> 4;
+  const int k_base = c * kKRow + 8 * h;
+  const int v_base = (4 * (q16 >> 1) + (r16 >> 2)) * kVRow + 16 * (q16 & 1) + 4 * (r16 & 3);
+
+  {
+    u32x4 kr[4], vr[4];
+    load_tile(kv_begin, kr, vr);
+    store_tile(0, kr, vr);
+  }
+  __syncthreads();
+
+  // m_run is the max used as the exponent base; it only moves when a row
+  // max exceeds it by more than kLazy in the exp2 domain, so probabilities
+  // stay below 2^kLazy and the accumulators are rescaled rarely.
+  auto step = [&](auto masked, const uint16_t *Kb, const uint16_t *Vb, int kt)
+                  __attribute__((always_inline)) {
+    constexpr bool kMasked = decltype(masked)::value;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      // S^T for both row blocks and both 16-key blocks of this 32-key step.
-      f32x4 s[2][2];
+    for (int kb = 0; kb < 2; ++kb) {
+      f32x16 s[2];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) s[rb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 16; ++i) s[rb][i] = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const bf16x8 kop = *reinterpret_cast<const bf16x8 *>(
-              &sK[(32 * ks + 16 * kb + m) * kKStride + kk * 32 + g * 8]);
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb)
-            s[rb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[rb][kk], s[rb][kb], 0, 0, 0);
-        }
-
-      bf16x8 pop[2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int limit = cache_len + row_tok[rb];  // last visible key
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float x = s[rb][kb][i] * scale_log2;
-            if (need_mask) {
-              const int key = kt + 32 * ks + 16 * kb + 4 * g + i;
-              if (key > limit) x = -INFINITY;
-            }
-            s[rb][kb][i] = x;
-            mloc = fmaxf(mloc, x);
-          }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        const float m_new = fmaxf(m_run[rb], mloc);
-        // A row whose keys so far are all masked keeps m = -inf; guard the
-        // exponent so that it contributes exact zeros.
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2f(m_run[rb] - m_use);
-        m_run[rb] = m_new;
-        float psum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = exp2f(s[rb][kb][i] - m_use);
-            s[rb][kb][i] = p;
-            psum += p;
-          }
-        l_run[rb] = l_run[rb] * alpha + psum;
-#pragma unroll
-        for (int db = 0; db < 8; ++db) acc[rb][db] *= alpha;
-        pop[rb] = pack_p(s[rb][0], s[rb][1]);
-      }
-
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        const uint16_t *vrow = &sVt[(16 * db + m) * kVtStride + 32 * ks + 4 * g];
-        const s16x4 a0 = *reinterpret_cast<const s16x4 *>(vrow);
-        const s16x4 a1 = *reinterpret_cast<const s16x4 *>(vrow + 16);
-        const bf16x8 vop = __builtin_bit_cast(
-            bf16x8, (__attribute__((ext_vector_type(8))) short){a0[0], a0[1], a0[2], a0[3],
-                                                                a1[0], a1[1], a1[2], a1[3]});
+      for (int kk = 0; kk < 8; ++kk) {
+        const bf16x8 kop =
+            *reinterpret_cast<const bf16x8 *>(Kb + k_base + 32 * kb * kKRow + 16 * kk);
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
-          acc[rb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[rb], acc[rb][db], 0, 0, 0);
+          s[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[rb][kk], s[rb], 0, 0, 0);
+      }
+
+      float mloc[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        if constexpr (kMasked) {
+          const int limit = cache_len + row_tok[rb];  // last visible key of this row
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = kt + 32 * kb + 8 * (i >> 2) + 4 * h + (i & 3);
+            if (key > limit) s[rb][i] = -INFINITY;
+          }
+        }
+        float m = s[rb][0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) m = fmaxf(m, s[rb][i]);
+        mloc[rb] = fmaxf(m, __shfl_xor(m, 32));
+      }
+      if (__any(mloc[0] * scale_log2 > m_run[0] * scale_log2 + kLazy ||
+                mloc[1] * scale_log2 > m_run[1] * scale_log2 + kLazy)) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          const float m_new = fmaxf(m_run[rb], mloc[rb]);
+          const float alpha = m_new == -INFINITY
+                                  ? 1.f
+                                  : __builtin_amdgcn_exp2f((m_run[rb] - m_new) * scale_log2);
+          m_run[rb] = m_new;
+          l_run[rb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < 4; ++db) acc[rb][db] *= alpha;
+        }
+      }
+
+      bf16x8 pop[2][2];  // [rb][kh]
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        // A row with every key so far masked keeps m = -inf: base 0 gives zeros.
+        const float mc = m_run[rb] == -INFINITY ? 0.f : m_run[rb] * scale_log2;
+        float psum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][i], scale_log2, -mc));
+          s[rb][i] = p;
+          psum += p;
+        }
+        pop[rb][0] = pack8(s[rb], 0);
+        pop[rb][1] = pack8(s[rb], 8);
+        l_run[rb] += psum;
+      }
+
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int kh2 = 0; kh2 < 2; ++kh2) {
+          const uint16_t *vp = Vb + v_base + (32 * kb + 16 * kh2) * kVRow + 32 * db;
+          const s16x4 lo = tr_read(vp);
+          const s16x4 hi = tr_read(vp + 8 * kVRow);
+          const s16x8 v8 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb)
+            acc[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, v8), pop[rb][kh2], acc[rb][db], 0, 0, 0);
+        }
+    }
+  };
+
+  // Tiles wholly below the diagonal need no mask; the rest (the diagonal
+  // tiles of the query chunk, always last) do. Two loops keep the two bodies
+  // apart (a per-tile choice between them doubles register pressure).
+  const int n_tiles = (kv_end - kv_begin + kKeys - 1) / kKeys;
+  int n_plain = (diag_begin - kv_begin) / kKeys;  // tiles ending at or before diag_begin
+  n_plain = n_plain < 0 ? 0 : (n_plain > n_tiles ? n_tiles : n_plain);
+  auto iterate = [&](auto masked, int t) __attribute__((always_inline)) {
+    const int kt = kv_begin + kKeys * t;
+    const int b = t & 1;
+    const bool has_next = t + 1 < n_tiles;
+    u32x4 kr[4], vr[4];
+    if (has_next) load_tile(kt + kKeys, kr, vr);
+    step(masked, sK[b], sV[b], kt);
+    if (has_next) {
+      store_tile(b ^ 1, kr, vr);
+      __syncthreads();
+    }
+  };
+  for (int t = 0; t < n_plain; ++t) iterate(std::false_type{}, t);
+  for (int t = n_plain; t < n_tiles; ++t) iterate(std::true_type{}, t);
+
+  // Epilogue: full row sums, then the output or the split's partial.
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const float lsum = l_run[rb] + __shfl_xor(l_run[rb], 32);
+    const int r = 64 * wave + 32 * rb + c;
+    if (slot < 0) {
+      const int i = row_tok[rb];
+      if (i >= q_end) continue;
+      const float inv = 1.0f / lsum;
+      uint16_t *dst =
+          out + seq * o_ss + static_cast<int64_t>(qs + i) * o_st + (h0 + r % G) * o_sh;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int d = 32 * db + 8 * i4 + 4 * h;
+          const uint32_t w0 = f32_to_bf16_rne(acc[rb][db][4 * i4] * inv) |
+                              (f32_to_bf16_rne(acc[rb][db][4 * i4 + 1] * inv) << 16);
+          const uint32_t w1 = f32_to_bf16_rne(acc[rb][db][4 * i4 + 2] * inv) |
+                              (f32_to_bf16_rne(acc[rb][db][4 * i4 + 3] * inv) << 16);
+          *reinterpret_cast<uint2 *>(dst + d) = make_uint2(w0, w1);
+        }
+    } else {
+      const int64_t pr = (static_cast<int64_t>(slot) * num_kv_heads + kvh) * kRows + r;
+      float *dst = ws_acc + pr * kHeadDim;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int d = 32 * db + 8 * i4 + 4 * h;
+          *reinterpret_cast<f32x4 *>(dst + d) =
+              f32x4{acc[rb][db][4 * i4], acc[rb][db][4 * i4 + 1], acc[rb][db][4 * i4 + 2],
+                    acc[rb][db][4 * i4 + 3]};
+        }
+      if (h == 0) {
+        ws_ml[pr * 2 + 0] = m_run[rb] == -INFINITY ? -INFINITY : m_run[rb] * scale_log2;
+        ws_ml[pr * 2 + 1] = lsum;
       }
     }
   }
+}
 
-  // Row sums across the four key groups, then normalise and store.
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    float lsum = l_run[rb];
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-    const float inv = 1.0f / lsum;
-    const int r = 32 * wave + 16 * rb + m;
-    const int i = row_tok[rb];
-    if (i >= q_end) continue;
-    const int h = h0 + r % G;
-    uint16_t *dst = out + seq * o_ss + static_cast<int64_t>(qs + i) * o_st + h * o_sh;
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const uint32_t w0 = f32_to_bf16_rne(acc[rb][db][0] * inv) |
-                          (f32_to_bf16_rne(acc[rb][db][1] * inv) << 16);
-      const uint32_t w1 = f32_to_bf16_rne(acc[rb][db][2] * inv) |
-                          (f32_to_bf16_rne(acc[rb][db][3] * inv) << 16);
-      uint32_t *d = reinterpret_cast<uint32_t *>(dst + 16 * db + 4 * g);
-      d[0] = w0;
-      d[1] = w1;
-    }
+// Combines the splits of a query tile: grid (kv head, merge item, 64 groups
+// of 4 rows), 512 threads = 4 rows x 128 dims.
+// Item = {seq, q_begin, q_end, first_slot, num_splits, 0, 0, 0}.
+template <int G>
+__global__ __launch_bounds__(512) void prefill_merge_kernel(
+    uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
+    const int32_t *__restrict__ q_start, const int32_t *__restrict__ items,
+    const float *__restrict__ ws_acc, const float *__restrict__ ws_ml, int num_kv_heads) {
+  const int32_t *it = items + 8 * blockIdx.y;
+  const int kvh = blockIdx.x;
+  const int seq = it[0];
+  const int q_begin = it[1];
+  const int q_end = it[2];
+  const int first = it[3];
+  const int nsplit = it[4];
+  const int r = 4 * blockIdx.z + (threadIdx.x >> 7);
+  const int d = threadIdx.x & 127;
+  const int i = q_begin + r / G;
+  if (i >= q_end) return;
+  float mx = -INFINITY, lsum = 0.f, a = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const int64_t pr = (static_cast<int64_t>(first + s) * num_kv_heads + kvh) * kRows + r;
+    const float m = ws_ml[pr * 2];
+    if (m == -INFINITY) continue;
+    const float nm = fmaxf(mx, m);
+    const float f_old = mx == -INFINITY ? 0.f : exp2f(mx - nm);
+    const float f_new = exp2f(m - nm);
+    lsum = lsum * f_old + f_new * ws_ml[pr * 2 + 1];
+    a = a * f_old + f_new * ws_acc[pr * kHeadDim + d];
+    mx = nm;
   }
+  const int64_t qs = q_start[seq];
+  out[seq * o_ss + (qs + i) * o_st + (kvh * G + r % G) * o_sh + d] =
+      static_cast<uint16_t>(f32_to_bf16_rne(a / lsum));
 }
 
 template <int G>
-void launch_prefill(hipStream_t st, dim3 grid, const uint16_t *q, int64_t q_ss,
-                    int64_t q_st, int64_t q_sh, uint16_t *out, int64_t o_ss,
-                    int64_t o_st, int64_t o_sh, const uint16_t *k_pool,
-                    const uint16_t *v_pool, int64_t pool_hs,
-                    const int32_t *page_table, int64_t pt_stride,
-                    const int32_t *q_start, const int32_t *kv_lens,
-                    const int32_t *items, int page_size, float scale_log2) {
-  hipLaunchKernelGGL(prefill_kernel<G>, grid, dim3(256), 0, st, q, q_ss, q_st,
-                     q_sh, out, o_ss, o_st, o_sh, k_pool, v_pool, pool_hs,
-                     page_table, pt_stride, q_start, kv_lens, items,
-                     page_size, scale_log2);
+void launch_prefill(hipStream_t st, int num_kv_heads, int n_items, int n_merge,
+                    const uint16_t *q, int64_t q_ss, int64_t q_st, int64_t q_sh, uint16_t *out,
+                    int64_t o_ss, int64_t o_st, int64_t o_sh, const uint16_t *k_pool,
+                    const uint16_t *v_pool, int64_t pool_hs, const int32_t *page_table,
+                    int64_t pt_stride, const int32_t *q_start, const int32_t *kv_lens,
+                    const int32_t *items, const int32_t *merge_items, float *ws_acc,
+                    float *ws_ml, int page_shift, float scale_log2) {
+  hipLaunchKernelGGL(prefill_kernel<G>, dim3(num_kv_heads, n_items), dim3(256), 0, st, q, q_ss,
+                     q_st, q_sh, out, o_ss, o_st, o_sh, k_pool, v_pool, pool_hs, page_table,
+                     pt_stride, q_start, kv_lens, items, ws_acc, ws_ml, num_kv_heads, page_shift,
+                     scale_log2);
+  if (n_merge > 0)
+    hipLaunchKernelGGL(prefill_merge_kernel<G>, dim3(num_kv_heads, n_merge, kRows / 4),
+                       dim3(512), 0, st, out, o_ss, o_st, o_sh, q_start, merge_items, ws_acc,
+                       ws_ml, num_kv_heads);
 }
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 }  // namespace
 }  // namespace hy
 
 using hy::kHeadDim;
 
+extern "C" int64_t hy_prefill_workspace_bytes(int32_t n_slots, int32_t num_kv_heads,
+                                              int32_t head_dim) {
+  if (n_slots <= 0) return 0;
+  const int64_t rows = static_cast<int64_t>(n_slots) * num_kv_heads * hy::kRows;
+  return hy::align256(rows * head_dim * 4) + hy::align256(rows * 2 * 4);
+}
+
 extern "C" int hy_paged_prefill(
-    const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
-    int64_t q_stride_head, void *out, int64_t o_stride_seq,
-    int64_t o_stride_tok, int64_t o_stride_head, const void *k_pool,
-    const void *v_pool, int64_t pool_head_stride, const int32_t *page_table,
-    int64_t page_table_stride, const int32_t *q_start, const int32_t *kv_lens,
-    const int32_t *prefill_items, int32_t n_prefill, int32_t num_seqs,
-    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-    int32_t page_size, float scale, void *stream) {
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok, int64_t q_stride_head,
+    void *out, int64_t o_stride_seq, int64_t o_stride_tok, int64_t o_stride_head,
+    const void *k_pool, const void *v_pool, int64_t pool_head_stride,
+    const int32_t *page_table, int64_t page_table_stride, const int32_t *q_start,
+    const int32_t *kv_lens, const int32_t *prefill_items, int32_t n_prefill,
+    const int32_t *merge_items, int32_t n_merge, int32_t n_slots, void *workspace,
+    int64_t workspace_bytes, int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t page_size, float scale, void *stream) {
   hy::clear_error();
   HY_REQUIRE(num_seqs >= 1, "num_seqs must be positive");
+  HY_REQUIRE(scale > 0.f, "softmax scale must be positive");
   HY_REQUIRE(num_kv_heads >= 1 && num_q_heads >= num_kv_heads &&
                  num_q_heads % num_kv_heads == 0,
              "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",
              num_q_heads, num_kv_heads);
-  HY_REQUIRE_SUPPORTED(head_dim == kHeadDim, "head_dim %d unsupported (need %d)",
-                       head_dim, kHeadDim);
-  HY_REQUIRE_SUPPORTED(page_size >= 32 && page_size % 32 == 0,
-                       "page_size %d unsupported (multiple of 32 required)", page_size);
-  HY_REQUIRE(n_prefill >= 0, "n_prefill must be non-negative");
+  HY_REQUIRE_SUPPORTED(head_dim == kHeadDim, "head_dim %d unsupported (need %d)", head_dim,
+                       kHeadDim);
+  HY_REQUIRE_SUPPORTED(page_size >= 32 && (page_size & (page_size - 1)) == 0,
+                       "page_size %d unsupported (power of two >= 32 required)", page_size);
+  HY_REQUIRE(n_prefill >= 0 && n_merge >= 0 && n_slots >= 0, "item counts must be non-negative");
+  HY_REQUIRE((n_merge == 0) == (n_slots == 0),
+             "n_merge and n_slots must be both zero or both positive");
   if (n_prefill == 0) return HY_OK;
-  HY_REQUIRE(q && out && k_pool && v_pool && page_table && q_start && kv_lens &&
-                 prefill_items,
+  HY_REQUIRE(q && out && k_pool && v_pool && page_table && q_start && kv_lens && prefill_items,
              "hy_paged_prefill: null pointer argument");
+  HY_REQUIRE(n_merge == 0 || merge_items, "merge_items is NULL");
+  const int64_t need = hy_prefill_workspace_bytes(n_slots, num_kv_heads, head_dim);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    hy::set_error("workspace too small: need %lld bytes, got %lld",
+                  static_cast<long long>(need), static_cast<long long>(workspace_bytes));
+    return HY_ENOSPACE;
+  }
+  float *ws_acc = nullptr, *ws_ml = nullptr;
+  if (need > 0) {
+    const int64_t rows = static_cast<int64_t>(n_slots) * num_kv_heads * hy::kRows;
+    ws_acc = static_cast<float *>(workspace);
+    ws_ml = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                      hy::align256(rows * head_dim * 4));
+  }
   const int G = num_q_heads / num_kv_heads;
   const float scale_log2 = scale * hy::kLog2e;
+  const int page_shift = __builtin_ctz(static_cast<unsigned>(page_size));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  dim3 grid(n_prefill, num_kv_heads);
   const uint16_t *qq = static_cast<const uint16_t *>(q);
   uint16_t *oo = static_cast<uint16_t *>(out);
   const uint16_t *kp = static_cast<const uint16_t *>(k_pool);
   const uint16_t *vp = static_cast<const uint16_t *>(v_pool);
-#define HY_PREFILL_CASE(GG)                                                     \
-  case GG:                                                                      \
-    hy::launch_prefill<GG>(st, grid, qq, q_stride_seq, q_stride_tok,            \
-                           q_stride_head, oo, o_stride_seq, o_stride_tok,       \
-                           o_stride_head, kp, vp, pool_head_stride, page_table, \
-                           page_table_stride, q_start, kv_lens, prefill_items,  \
-                           page_size, scale_log2);                              \
+#define HY_PREFILL_CASE(GG)                                                                   \
+  case GG:                                                                                    \
+    hy::launch_prefill<GG>(st, num_kv_heads, n_prefill, n_merge, qq, q_stride_seq,            \
+                           q_stride_tok, q_stride_head, oo, o_stride_seq, o_stride_tok,        \
+                           o_stride_head, kp, vp, pool_head_stride, page_table,               \
+                           page_table_stride, q_start, kv_lens, prefill_items, merge_items,   \
+                           ws_acc, ws_ml, page_shift, scale_log2);                            \
     break;
   switch (G) {
     HY_PREFILL_CASE(1)

@@ -14,7 +14,10 @@ from typing import Optional
 import numpy as np
 
 LIB_NAME = "libhayate_attn.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# HAYATE_ATTN_LIB may point at another build of the same library.
+LIB_PATH = os.environ.get(
+    "HAYATE_ATTN_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+)
 
 HY_OK = 0
 HY_EINVAL = -1
@@ -52,19 +55,22 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     "hy_plan_tick": (
-        [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _I32, _P],
+        [_P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _I32, _P, _I32, _P,
+         _I32, _P],
         ctypes.c_int,
     ),
-    "hy_decode_workspace_bytes": ([_I32, _I32, _I32, _I32, _I32], ctypes.c_int64),
+    "hy_decode_workspace_bytes": ([_I32, _I32, _I32], ctypes.c_int64),
     "hy_paged_decode": (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64,
-         _P, _P, _I32, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32,
+         _P, _P, _I32, _P, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32,
          _F32, _P],
         ctypes.c_int,
     ),
+    "hy_prefill_workspace_bytes": ([_I32, _I32, _I32], ctypes.c_int64),
     "hy_paged_prefill": (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64,
-         _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P],
+         _P, _P, _P, _I32, _P, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32,
+         _F32, _P],
         ctypes.c_int,
     ),
 }
@@ -119,13 +125,15 @@ def check(rc: int, what: str) -> None:
 class TickPlan:
     """Host copy of one tick's work lists (hy_plan_tick)."""
 
-    __slots__ = ("decode", "prefill", "n_groups", "n_slots")
+    __slots__ = ("decode", "merge", "n_slots", "prefill", "prefill_merge", "n_prefill_slots")
 
-    def __init__(self, decode, prefill, n_groups, n_slots):
-        self.decode = decode      # int32 (n, 8)
-        self.prefill = prefill    # int32 (n, 4)
-        self.n_groups = n_groups
+    def __init__(self, decode, merge, n_slots, prefill, prefill_merge, n_prefill_slots):
+        self.decode = decode                # int32 (n, 4) {seq, tok_begin, tok_end, slot}
+        self.merge = merge                  # int32 (n, 4) {seq, first_slot, num_splits, 0}
         self.n_slots = n_slots
+        self.prefill = prefill              # int32 (n, 8) {seq, q0, q1, kv0, kv1, slot, 0, 0}
+        self.prefill_merge = prefill_merge  # int32 (n, 8) {seq, q0, q1, first_slot, splits, ..}
+        self.n_prefill_slots = n_prefill_slots
 
 
 def plan_tick(
@@ -137,33 +145,38 @@ def plan_tick(
     num_cus: int,
     tokens_per_split: int = 0,
 ) -> TickPlan:
-    """Run the native tick planner.
-
-    decode rows: {seq, tok_begin, tok_end, slot, group, first_slot,
-    num_splits, 0}; prefill rows: {seq, q_begin, q_end, 0}.
-    """
+    """Run the native tick planner."""
     q_lens = np.ascontiguousarray(q_lens, dtype=np.int32)
     kv_lens = np.ascontiguousarray(kv_lens, dtype=np.int32)
     n = int(q_lens.shape[0])
     group = max(1, num_q_heads // max(1, num_kv_heads))
-    tile = max(1, 128 // group)
+    tile = max(1, 256 // group)
     split_floor = 32 if tokens_per_split <= 0 else max(32, tokens_per_split)
-    dec_cap = int(sum(int(k) // split_floor + 1 for k, q in zip(kv_lens, q_lens) if q == 1)) + 1
-    pre_cap = int(sum((int(q) + tile - 1) // tile for q in q_lens if q > 1)) + 1
-    dec = np.zeros((dec_cap, 8), dtype=np.int32)
-    pre = np.zeros((pre_cap, 4), dtype=np.int32)
-    counts = np.zeros(4, dtype=np.int32)
+    dec_mask = q_lens == 1
+    pre_mask = q_lens > 1
+    dec_cap = int((kv_lens[dec_mask].astype(np.int64) // split_floor + 1).sum()) + 1
+    n_tiles = int(((q_lens[pre_mask].astype(np.int64) + tile - 1) // tile).sum())
+    max_steps = int((kv_lens.max() + 63) // 64) if n else 1
+    pre_cap = n_tiles * max(1, max_steps // 4 + 1) + 1
+    dec = np.zeros((dec_cap, 4), dtype=np.int32)
+    mrg = np.zeros((n + 1, 4), dtype=np.int32)
+    pre = np.zeros((pre_cap, 8), dtype=np.int32)
+    pmrg = np.zeros((n_tiles + 1, 8), dtype=np.int32)
+    counts = np.zeros(6, dtype=np.int32)
     rc = lib().hy_plan_tick(
         q_lens.ctypes.data, kv_lens.ctypes.data, n, num_q_heads, num_kv_heads,
         page_size, num_cus, tokens_per_split, dec.ctypes.data, dec_cap,
-        pre.ctypes.data, pre_cap, counts.ctypes.data,
+        mrg.ctypes.data, n + 1, pre.ctypes.data, pre_cap, pmrg.ctypes.data, n_tiles + 1,
+        counts.ctypes.data,
     )
     check(rc, "hy_plan_tick")
-    nd, ng, npf, ns = (int(x) for x in counts)
-    return TickPlan(dec[:nd].copy(), pre[:npf].copy(), ng, ns)
+    nd, nm, ns, npf, npm, nps = (int(x) for x in counts)
+    return TickPlan(dec[:nd].copy(), mrg[:nm].copy(), ns, pre[:npf].copy(), pmrg[:npm].copy(), nps)
 
 
-def decode_workspace_bytes(n_slots: int, n_groups: int, num_q_heads: int,
-                           num_kv_heads: int, head_dim: int) -> int:
-    return int(lib().hy_decode_workspace_bytes(n_slots, n_groups, num_q_heads,
-                                               num_kv_heads, head_dim))
+def decode_workspace_bytes(n_slots: int, num_q_heads: int, head_dim: int) -> int:
+    return int(lib().hy_decode_workspace_bytes(n_slots, num_q_heads, head_dim))
+
+
+def prefill_workspace_bytes(n_slots: int, num_kv_heads: int, head_dim: int) -> int:
+    return int(lib().hy_prefill_workspace_bytes(n_slots, num_kv_heads, head_dim))

@@ -87,27 +87,37 @@ def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
 
 
 class _DevicePlan:
-    """One tick's work lists on the device plus the split-K workspace (fp32
-    partials and arrival counters; the counters start at zero and every
-    decode call leaves them at zero)."""
+    """One tick's work lists on the device plus the split workspaces."""
 
     def __init__(self, host: "_native.TickPlan", num_q_heads: int, num_kv_heads: int,
                  head_dim: int, device: torch.device):
         self.host = host
         self.n_decode = len(host.decode)
-        self.n_prefill = len(host.prefill)
-        self.n_groups = host.n_groups
+        self.n_merge = len(host.merge)
         self.n_slots = host.n_slots
-        packed = np.concatenate([host.decode.reshape(-1), host.prefill.reshape(-1)])
+        self.n_prefill = len(host.prefill)
+        self.n_prefill_merge = len(host.prefill_merge)
+        self.n_prefill_slots = host.n_prefill_slots
+        parts = [host.decode, host.merge, host.prefill, host.prefill_merge]
+        packed = np.concatenate([p.reshape(-1) for p in parts])
         dev = torch.from_numpy(np.ascontiguousarray(packed, dtype=np.int32)).to(device)
-        self.decode = dev[: host.decode.size]
-        self.prefill = dev[host.decode.size :]
-        self.workspace_bytes = _native.decode_workspace_bytes(
-            self.n_slots, self.n_groups, num_q_heads, num_kv_heads, head_dim
-        )
+        views, off = [], 0
+        for p in parts:
+            views.append(dev[off : off + p.size])
+            off += p.size
+        self.decode, self.merge, self.prefill, self.prefill_merge = views
+        self.workspace_bytes = _native.decode_workspace_bytes(self.n_slots, num_q_heads, head_dim)
         self.workspace = (
-            torch.zeros(self.workspace_bytes // 4, dtype=torch.int32, device=device)
+            torch.empty(self.workspace_bytes // 4, dtype=torch.float32, device=device)
             if self.workspace_bytes
+            else None
+        )
+        self.prefill_workspace_bytes = _native.prefill_workspace_bytes(
+            self.n_prefill_slots, num_kv_heads, head_dim
+        )
+        self.prefill_workspace = (
+            torch.empty(self.prefill_workspace_bytes // 4, dtype=torch.float32, device=device)
+            if self.prefill_workspace_bytes
             else None
         )
 
@@ -357,7 +367,7 @@ class PagedKVBatch:
                 k_layer.data_ptr(), v_layer.data_ptr(), hs,
                 self.page_table.data_ptr(), self.page_table.stride(0),
                 self.q_start.data_ptr(), plan.decode.data_ptr(), plan.n_decode,
-                plan.n_groups, plan.n_slots,
+                plan.merge.data_ptr() if plan.n_merge else None, plan.n_merge, plan.n_slots,
                 None if plan.workspace is None else plan.workspace.data_ptr(),
                 plan.workspace_bytes, self.num_seqs, num_q_heads,
                 self.num_kv_heads, self.head_dim, self.page_size, float(scale),
@@ -370,7 +380,11 @@ class PagedKVBatch:
                 k_layer.data_ptr(), v_layer.data_ptr(), hs,
                 self.page_table.data_ptr(), self.page_table.stride(0),
                 self.q_start.data_ptr(), self.kv_lens.data_ptr(),
-                plan.prefill.data_ptr(), plan.n_prefill, self.num_seqs, num_q_heads,
+                plan.prefill.data_ptr(), plan.n_prefill,
+                plan.prefill_merge.data_ptr() if plan.n_prefill_merge else None,
+                plan.n_prefill_merge, plan.n_prefill_slots,
+                None if plan.prefill_workspace is None else plan.prefill_workspace.data_ptr(),
+                plan.prefill_workspace_bytes, self.num_seqs, num_q_heads,
                 self.num_kv_heads, self.head_dim, self.page_size, float(scale),
                 stream,
             )

@@ -23,7 +23,7 @@
  * can be passed without a copy. q_start has num_seqs + 1 entries
  * (cumulative query lengths, q_start[0] == 0).
  *
- * Supported geometry: head_dim == 128, page_size a multiple of 32,
+ * Supported geometry: head_dim == 128, page_size a power of two >= 32,
  * num_q_heads / num_kv_heads in {1, 2, 4, 8, 16}; bf16 storage.
  */
 #ifndef HAYATE_ATTN_H
@@ -118,19 +118,25 @@ int hy_page_scatter(void *pool, int64_t pool_layer_stride,
  * Tick planner (host only, no device access). Given per-sequence query
  * lengths and KV lengths (kv_len = cache_len + q_len), split the work of
  * one attention call into:
- *   decode items  (q_len == 1): int32[n][8] =
- *                 {seq, tok_begin, tok_end, slot, group, first_slot,
- *                  num_splits, 0}
- *                 tok_begin is a multiple of 32; a sequence with one split
- *                 has slot = group = -1 and writes its output directly;
- *                 otherwise its splits own workspace slots first_slot ..
- *                 first_slot + num_splits - 1 and share merge group `group`;
- *   prefill items (q_len > 1):  int32[n][4] = {seq, q_begin, q_end, 0}
- *                 query tiles of the sequence, most keys first.
- * counts_out receives {n_decode, n_groups, n_prefill, n_slots}.
+ *   decode items  (q_len == 1): int32[n][4] = {seq, tok_begin, tok_end, slot}
+ *                 token ranges of equal length (tok_begin a multiple of 32),
+ *                 longest first; slot = -1 writes the output directly,
+ *                 otherwise the split's partial goes to workspace slot `slot`;
+ *   merge items   int32[n][4] = {seq, first_slot, num_splits, 0}, one per
+ *                 decode sequence with more than one split;
+ *   prefill items (q_len > 1): int32[n][8] =
+ *                 {seq, q_begin, q_end, kv_begin, kv_end, slot, 0, 0}:
+ *                 query tiles of 256 / G tokens, each over one range of keys
+ *                 (kv_begin a multiple of 64), most keys first; slot as for
+ *                 decode items;
+ *   prefill merge items int32[n][8] =
+ *                 {seq, q_begin, q_end, first_slot, num_splits, 0, 0, 0}.
+ * Split lengths are chosen by simulating the longest-first dispatch of the
+ * work onto num_cus CUs. counts_out receives {n_decode, n_merge,
+ * n_decode_slots, n_prefill, n_prefill_merge, n_prefill_slots}.
  * Capacities are in items; returns HY_ENOSPACE if one is too small.
- * target_tokens_per_split sets the decode split length (rounded up to a
- * multiple of 32); <= 0 picks one from the total decode work and num_cus.
+ * target_tokens_per_split > 0 fixes the decode split length (rounded up to
+ * a multiple of 32) instead.
  * Replaces the per-forward metadata of PagedKVCacheManager.begin_batch
  * (paged_cache.py:202-293: page table, cache_lens, kv_lens, block mask).
  */
@@ -138,29 +144,25 @@ int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
                  int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                  int32_t page_size, int32_t num_cus,
                  int32_t target_tokens_per_split, int32_t *decode_items,
-                 int32_t decode_capacity, int32_t *prefill_items,
-                 int32_t prefill_capacity, int32_t *counts_out);
+                 int32_t decode_capacity, int32_t *merge_items,
+                 int32_t merge_capacity, int32_t *prefill_items,
+                 int32_t prefill_capacity, int32_t *prefill_merge_items,
+                 int32_t prefill_merge_capacity, int32_t *counts_out);
 
-/*
- * Split-K workspace bytes: n_slots fp32 partials (acc[head_dim], max, sum
- * per query head) plus one int32 arrival counter per (group, kv head).
- * The counters must be zero before the first call; every call leaves them
- * zero again.
- */
-int64_t hy_decode_workspace_bytes(int32_t n_slots, int32_t n_groups,
-                                  int32_t num_q_heads, int32_t num_kv_heads,
+/* Split-K workspace bytes for n_slots fp32 partials (acc[head_dim], max,
+ * sum per query head). */
+int64_t hy_decode_workspace_bytes(int32_t n_slots, int32_t num_q_heads,
                                   int32_t head_dim);
 
 /*
  * Paged GQA decode attention for sequences with one query token each
- * (items from hy_plan_tick), one kernel launch. Each workgroup covers one
- * decode item and one kv head, loads every K/V row of its token range once
- * and applies it to all num_q_heads / num_kv_heads query heads; for a
- * sequence with several splits, the workgroup that finishes last merges the
- * fp32 partials of all splits (log-sum-exp) and writes the output.
- * Causal semantics: query i of sequence b sees logical keys
- * k <= cache_len_b + i with kv_len = cache_len + 1 (paged_cache.py:266-271).
- * Calls that share a workspace must not overlap in time.
+ * (items from hy_plan_tick). Each workgroup covers one decode item and one
+ * kv head, loads every K/V row of its token range once and applies it to
+ * all num_q_heads / num_kv_heads query heads (QK^T and PV on MFMA). When
+ * n_merge > 0 a second launch on the same stream merges the fp32 partials
+ * of split sequences (log-sum-exp) into the output.
+ * Causal semantics: the query of sequence b at position kv_len - 1 sees
+ * every key k < kv_len (paged_cache.py:266-271).
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T == 1.
  */
 int hy_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
@@ -170,17 +172,23 @@ int hy_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
                     int64_t pool_head_stride, const int32_t *page_table,
                     int64_t page_table_stride, const int32_t *q_start,
                     const int32_t *decode_items, int32_t n_decode,
-                    int32_t n_groups, int32_t n_slots, void *workspace,
-                    int64_t workspace_bytes, int32_t num_seqs,
-                    int32_t num_q_heads, int32_t num_kv_heads,
+                    const int32_t *merge_items, int32_t n_merge,
+                    int32_t n_slots, void *workspace, int64_t workspace_bytes,
+                    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t page_size, float scale,
                     void *stream);
+
+/* Prefill split workspace bytes for n_slots partials (fp32 acc[head_dim],
+ * max, sum for each of the 256 rows of a query tile, per kv head). */
+int64_t hy_prefill_workspace_bytes(int32_t n_slots, int32_t num_kv_heads,
+                                   int32_t head_dim);
 
 /*
  * Paged chunked-prefill causal attention (bf16 MFMA) for sequences with
  * q_len > 1 (prefill items from hy_plan_tick): query i of sequence b at
- * logical position cache_lens[b] + i sees every cached prefix key and the
- * chunk's keys up to itself. K/V are read through the page table.
+ * logical position cache_len_b + i sees every cached prefix key and the
+ * chunk's keys up to itself. K/V are read through the page table. When
+ * n_merge > 0 a second launch on the same stream merges the splits.
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T > 1.
  */
 int hy_paged_prefill(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
@@ -190,9 +198,12 @@ int hy_paged_prefill(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
                      int64_t pool_head_stride, const int32_t *page_table,
                      int64_t page_table_stride, const int32_t *q_start,
                      const int32_t *kv_lens, const int32_t *prefill_items,
-                     int32_t n_prefill, int32_t num_seqs, int32_t num_q_heads,
-                     int32_t num_kv_heads, int32_t head_dim,
-                     int32_t page_size, float scale, void *stream);
+                     int32_t n_prefill, const int32_t *merge_items,
+                     int32_t n_merge, int32_t n_slots, void *workspace,
+                     int64_t workspace_bytes, int32_t num_seqs,
+                     int32_t num_q_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t page_size, float scale,
+                     void *stream);
 
 #ifdef __cplusplus
 }

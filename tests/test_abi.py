@@ -47,44 +47,59 @@ def test_plan_decode_covers_every_token_once(split):
     p = plan([1] * 40, kv, split=split)
     dec = p.decode
     assert len(p.prefill) == 0
-    groups = set()
+    lengths = dec[:, 2] - dec[:, 1]
+    assert (lengths[:-1] >= lengths[1:]).all()  # longest first
+    merged = {int(m[0]): m for m in p.merge}
     for b in range(40):
         items = dec[dec[:, 0] == b]
+        items = items[np.argsort(items[:, 1])]
         assert items[0, 1] == 0 and items[-1, 2] == kv[b]
         assert (items[1:, 1] == items[:-1, 2]).all()
         assert (items[:, 1] % 32 == 0).all() and (items[:, 2] > items[:, 1]).all()
-        assert (items[:, 6] == len(items)).all()
         if len(items) == 1:
-            assert items[0, 3] == -1 and items[0, 4] == -1
+            assert items[0, 3] == -1 and b not in merged
         else:
-            first = items[0, 5]
-            assert (items[:, 3] == np.arange(first, first + len(items))).all()
-            assert len(set(items[:, 4])) == 1
-            groups.add(int(items[0, 4]))
-    assert groups == set(range(p.n_groups))
-    assert p.n_slots == int((dec[:, 3] >= 0).sum())
+            m = merged[b]
+            assert m[2] == len(items)
+            assert (items[:, 3] == np.arange(m[1], m[1] + len(items))).all()
+    assert p.n_slots == int((dec[:, 3] >= 0).sum()) == int(p.merge[:, 2].sum())
 
 
 def test_plan_splits_are_balanced():
     p = plan([1], [300], split=256)
-    assert [tuple(r[1:3]) for r in p.decode] == [(0, 160), (160, 300)]
+    assert sorted(tuple(r[1:3]) for r in p.decode) == [(0, 160), (160, 300)]
 
 
-def test_plan_prefill_tiles_longest_first():
-    p = plan([512, 512, 1, 3], [512, 4096, 700, 10])
+def test_plan_prefill_tiles_cover_every_query_and_key_once():
+    q = [512, 512, 1, 3, 512]
+    kv = [512, 4096, 700, 10, 8192]
+    p = plan(q, kv)
     dec, pre = p.decode, p.prefill
     assert len(dec) >= 1 and (dec[:, 0] == 2).all()
-    tile = 128 // 4
-    assert len(pre) == 2 * (512 // tile) + 1
-    keys = [(4096 - 512 if s == 1 else (10 - 3 if s == 3 else 0)) + q1 for s, q0, q1, _ in pre]
-    assert keys == sorted(keys, reverse=True)
-    covered = {}
-    for s, q0, q1, _ in pre:
-        covered.setdefault(int(s), []).append((int(q0), int(q1)))
-    for s, ql in [(0, 512), (1, 512), (3, 3)]:
-        spans = sorted(covered[s])
-        assert spans[0][0] == 0 and spans[-1][1] == ql
-        assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
+    tile = 256 // 4
+    lengths = pre[:, 4] - pre[:, 3]
+    assert (lengths[:-1] >= lengths[1:]).all()  # longest first
+    assert (pre[:, 3] % 64 == 0).all()
+    merges = {(int(m[0]), int(m[1])): m for m in p.prefill_merge}
+    for s_, ql in [(0, 512), (1, 512), (3, 3), (4, 512)]:
+        cache = kv[s_] - ql
+        rows = pre[pre[:, 0] == s_]
+        for q0 in range(0, ql, tile):
+            q1 = min(ql, q0 + tile)
+            parts = rows[(rows[:, 1] == q0)]
+            assert (parts[:, 2] == q1).all()
+            parts = parts[np.argsort(parts[:, 3])]
+            assert parts[0, 3] == 0 and parts[-1, 4] == cache + q1
+            assert (parts[1:, 3] == parts[:-1, 4]).all()
+            if len(parts) == 1:
+                assert parts[0, 5] == -1 and (s_, q0) not in merges
+            else:
+                m = merges[(s_, q0)]
+                assert m[2] == q1 and m[4] == len(parts)
+                assert sorted(parts[:, 5]) == list(range(m[3], m[3] + len(parts)))
+    assert p.n_prefill_slots == int((pre[:, 5] >= 0).sum())
+    # the 8192-token tile must have been split to balance the tick
+    assert len(merges) > 0
 
 
 def test_plan_rejects_bad_input():
@@ -97,9 +112,9 @@ def test_plan_rejects_bad_input():
 
 
 def test_workspace_size():
-    assert _native.decode_workspace_bytes(0, 0, 32, 8, 128) == 0
-    n = _native.decode_workspace_bytes(3, 1, 32, 8, 128)
-    assert n % 256 == 0 and n >= 3 * 32 * 130 * 4 + 8 * 4
+    assert _native.decode_workspace_bytes(0, 32, 128) == 0
+    n = _native.decode_workspace_bytes(3, 32, 128)
+    assert n % 256 == 0 and n >= 3 * 32 * 130 * 4
 
 
 def test_entry_points_validate_before_touching_the_device():
@@ -118,15 +133,16 @@ def test_entry_points_validate_before_touching_the_device():
     assert rc == _native.HY_EUNSUPPORTED
     # GQA group 3 is not built
     rc = lib.hy_paged_decode(fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, 0, fake, 0, fake,
-                             fake, 1, 0, 0, None, 0, 1, 6, 2, 128, 128, 0.1, None)
+                             fake, 1, None, 0, 0, None, 0, 1, 6, 2, 128, 128, 0.1, None)
     assert rc == _native.HY_EUNSUPPORTED
     # workspace too small for the slots
     rc = lib.hy_paged_decode(fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, 0, fake, 0, fake,
-                             fake, 2, 1, 2, fake, 100, 1, 32, 8, 128, 128, 0.1, None)
+                             fake, 2, fake, 1, 2, fake, 100, 1, 32, 8, 128, 128, 0.1, None)
     assert rc == _native.HY_ENOSPACE
     with pytest.raises(MemoryError):
         _native.check(rc, "hy_paged_decode")
     # nothing to do is success, even with null buffers
     assert lib.hy_paged_prefill(None, 0, 0, 0, None, 0, 0, 0, None, None, 0, None, 0, None,
-                                None, None, 0, 1, 32, 8, 128, 128, 0.1, None) == 0
+                                None, None, 0, None, 0, 0, None, 0, 1, 32, 8, 128, 128, 0.1,
+                                None) == 0
     assert lib.hy_last_error() == b""
