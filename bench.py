@@ -62,6 +62,20 @@ def time_workload(name, steps, warmup, layers, split=0):
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(steps)]
+    # events bracketing the attention kernels, created before the timed region
+    timed = ("hy_paged_decode", "hy_paged_prefill")
+    pool = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                for _ in range(steps)] for n in timed}
+    used = {n: 0 for n in timed}
+
+    def hook(kname, after):
+        if kname in pool:
+            pair = pool[kname][used[kname]]
+            pair[1 if after else 0].record(stream)
+            if after:
+                used[kname] += 1
+
+    batch.launch_hook = hook
     t0 = time.perf_counter()
     for i in range(steps):
         layer = i % layers
@@ -71,32 +85,44 @@ def time_workload(name, steps, warmup, layers, split=0):
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    batch.launch_hook = None
     attn_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
     step_ms = (t1 - t0) * 1e3 / steps
+    kernel_ms = {n: float(np.mean([a.elapsed_time(b) for a, b in pool[n][: used[n]]]))
+                 for n in timed if used[n]}
     out = {
         "workload": w.spec.description,
         "ms_per_step": step_ms,
         "attn_ms": attn_ms,
         "decode_bytes": w.decode_bytes(),
+        "decode_kernel_bytes": w.decode_bytes(include_append=False),
         "prefill_flops": w.prefill_flops(),
         "n_decode_items": plan.n_decode,
         "n_prefill_items": plan.n_prefill,
+        "kernel_ms": kernel_ms,
     }
     if out["decode_bytes"]:
         out["decode_GBps_step"] = out["decode_bytes"] / (step_ms * 1e-3) / 1e9
         out["decode_GBps_attn"] = out["decode_bytes"] / (attn_ms * 1e-3) / 1e9
         out["decode_frac_hbm"] = out["decode_GBps_attn"] / HBM_PEAK_GBS
+        if "hy_paged_decode" in kernel_ms and not out["prefill_flops"]:
+            out["decode_GBps_kernel"] = (out["decode_kernel_bytes"]
+                                         / (kernel_ms["hy_paged_decode"] * 1e-3) / 1e9)
     if out["prefill_flops"]:
         out["prefill_TFLOPs_attn"] = out["prefill_flops"] / (attn_ms * 1e-3) / 1e12
         out["prefill_frac_mfma"] = out["prefill_TFLOPs_attn"] / BF16_PEAK_TFLOPS
+        if "hy_paged_prefill" in kernel_ms and not out["decode_bytes"]:
+            out["prefill_TFLOPs_kernel"] = (out["prefill_flops"]
+                                            / (kernel_ms["hy_paged_prefill"] * 1e-3) / 1e12)
     del w, batch
     torch.cuda.empty_cache()
     return out
 
 
 def cpu_baseline(budget_s=10.0):
-    """Oracle decode attention on the host, 1 thread, over as many requests
-    of the batch-32 decode workload as fit in about `budget_s` seconds."""
+    """Oracle decode attention on the host, 1 thread, over the batch-32
+    decode workload: whole passes over its 32 requests until about
+    `budget_s` seconds of work are done."""
     from threadpoolctl import threadpool_limits
 
     from hayate_amd.workloads import make_workload
@@ -106,25 +132,41 @@ def cpu_baseline(budget_s=10.0):
     pk = R.torch_bf16_to_bits(w.manager.k_cache[0, 0])
     pv = R.torch_bf16_to_bits(w.manager.v_cache[0, 0])
     q = R.torch_bf16_to_bits(w.q)
+    del w.manager
+    torch.cuda.empty_cache()
     done_bytes = 0
-    n = 0
+    passes = 0
     torch.set_num_threads(1)
     with threadpool_limits(limits=1):
         t0 = time.perf_counter()
-        while n < len(w.q_lens) and time.perf_counter() - t0 < budget_s:
-            R.paged_attention(q[n : n + 1], pk, pv, [w.page_lists[n]], [w.cache_lens[n]], [1],
-                              128, dtype=np.float32)
-            done_bytes += (w.cache_lens[n] + 1) * 4096
-            n += 1
+        while time.perf_counter() - t0 < budget_s:
+            R.paged_attention(q, pk, pv, w.page_lists, w.cache_lens, w.q_lens, 128,
+                              dtype=np.float32)
+            done_bytes += w.decode_bytes()
+            passes += 1
         dt = time.perf_counter() - t0
     return {
-        "value": done_bytes / dt / 1e9,
+        "value": round(done_bytes / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"oracle float32 paged decode attention over the first {n} of 32 "
-                  f"requests of the batch-32 decode workload ({dt:.1f} s)",
+        "sample": f"oracle float32 paged decode attention, {passes} passes over the 32 requests "
+                  f"of the batch-32 decode workload ({dt:.1f} s, one thread)",
     }
+
+
+def traffic_from_profile(name):
+    """HBM bytes per launch of the dominant kernel, read from the committed
+    rocprofv3 --pmc summary profiles/<name>.md (FETCH_SIZE + WRITE_SIZE,
+    each calibrated against a plain 1 GiB copy), or None."""
+    path = os.path.join(ROOT, "profiles", f"{name}.md")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch ="):
+                return int(line.split("=", 1)[1])
+    return None
 
 
 def main():
@@ -179,11 +221,14 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(head["decode_GBps_attn"], 1),
+            "kernel": "decode_kernel<4> (hy_paged_decode)",
+            "achieved": round(head["decode_GBps_kernel"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(head["decode_frac_hbm"], 4),
-            "traffic": None,
+            "frac": round(head["decode_GBps_kernel"] / HBM_PEAK_GBS, 4),
+            "kernel_us": round(head["kernel_ms"]["hy_paged_decode"] * 1e3, 2),
+            "algorithmic_bytes": head["decode_kernel_bytes"],
+            "traffic": traffic_from_profile("decode_kernel_decode_b32"),
         },
     }
     if not args.no_cpu:

@@ -36,8 +36,9 @@
 // The end of a split merges the four waves in LDS and writes either the bf16
 // output (single split) or an fp32 partial (acc, max, sum) to the workspace;
 // decode_merge_kernel then combines the partials of each split sequence
-// (log-sum-exp). The merge is a second launch on the same stream: the kernel
-// boundary publishes the partials without any device-scope fence.
+// (log-sum-exp). The merge is a second launch (hy_paged_decode_merge) on the
+// same stream: the kernel boundary publishes the partials without any
+// device-scope fence.
 
 #include "hy_common.h"
 
@@ -409,8 +410,8 @@ extern "C" int hy_paged_decode(
     void *out, int64_t o_stride_seq, int64_t o_stride_tok, int64_t o_stride_head,
     const void *k_pool, const void *v_pool, int64_t pool_head_stride,
     const int32_t *page_table, int64_t page_table_stride, const int32_t *q_start,
-    const int32_t *decode_items, int32_t n_decode, const int32_t *merge_items,
-    int32_t n_merge, int32_t n_slots, void *workspace, int64_t workspace_bytes,
+    const int32_t *decode_items, int32_t n_decode, int32_t n_slots, void *workspace,
+    int64_t workspace_bytes,
     int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
     int32_t page_size, float scale, void *stream) {
   hy::clear_error();
@@ -424,13 +425,10 @@ extern "C" int hy_paged_decode(
                        kHeadDim);
   HY_REQUIRE_SUPPORTED(page_size >= 32 && (page_size & (page_size - 1)) == 0,
                        "page_size %d unsupported (power of two >= 32 required)", page_size);
-  HY_REQUIRE(n_decode >= 0 && n_merge >= 0 && n_slots >= 0, "item counts must be non-negative");
-  HY_REQUIRE((n_merge == 0) == (n_slots == 0),
-             "n_merge and n_slots must be both zero or both positive");
+  HY_REQUIRE(n_decode >= 0 && n_slots >= 0, "item counts must be non-negative");
   if (n_decode == 0) return HY_OK;
   HY_REQUIRE(q && out && k_pool && v_pool && page_table && q_start && decode_items,
              "hy_paged_decode: null pointer argument");
-  HY_REQUIRE(n_merge == 0 || merge_items, "merge_items is NULL");
   const int64_t need = hy_decode_workspace_bytes(n_slots, num_q_heads, head_dim);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     hy::set_error("workspace too small: need %lld bytes, got %lld",
@@ -471,12 +469,35 @@ extern "C" int hy_paged_decode(
       return HY_EUNSUPPORTED;
   }
 #undef HY_DECODE_CASE
-  if (int rc = hy::launch_status("hy_paged_decode")) return rc;
-  if (n_merge > 0) {
-    hipLaunchKernelGGL(hy::decode_merge_kernel, dim3(n_merge, num_q_heads), dim3(128), 0, st,
-                       oo, o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items,
-                       ws_acc, ws_ml, num_q_heads);
-    return hy::launch_status("hy_paged_decode (merge)");
+  return hy::launch_status("hy_paged_decode");
+}
+
+extern "C" int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,
+                                     int64_t o_stride_head, const int32_t *q_start,
+                                     const int32_t *merge_items, int32_t n_merge,
+                                     int32_t n_slots, const void *workspace,
+                                     int64_t workspace_bytes, int32_t num_q_heads,
+                                     int32_t head_dim, void *stream) {
+  hy::clear_error();
+  HY_REQUIRE(n_merge >= 0 && n_slots >= 0, "item counts must be non-negative");
+  if (n_merge == 0) return HY_OK;
+  HY_REQUIRE_SUPPORTED(head_dim == kHeadDim, "head_dim %d unsupported (need %d)", head_dim,
+                       kHeadDim);
+  HY_REQUIRE(out && q_start && merge_items && workspace,
+             "hy_paged_decode_merge: null pointer argument");
+  const int64_t need = hy_decode_workspace_bytes(n_slots, num_q_heads, head_dim);
+  if (workspace_bytes < need) {
+    hy::set_error("workspace too small: need %lld bytes, got %lld",
+                  static_cast<long long>(need), static_cast<long long>(workspace_bytes));
+    return HY_ENOSPACE;
   }
-  return HY_OK;
+  const float *ws_acc = static_cast<const float *>(workspace);
+  const float *ws_ml = reinterpret_cast<const float *>(
+      static_cast<const char *>(workspace) +
+      hy::align256(static_cast<int64_t>(n_slots) * num_q_heads * head_dim * 4));
+  hipLaunchKernelGGL(hy::decode_merge_kernel, dim3(n_merge, num_q_heads), dim3(128), 0,
+                     static_cast<hipStream_t>(stream), static_cast<uint16_t *>(out),
+                     o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items, ws_acc,
+                     ws_ml, num_q_heads);
+  return hy::launch_status("hy_paged_decode_merge");
 }

@@ -30,7 +30,8 @@
 //
 // A split whose item has slot >= 0 writes an fp32 partial (unnormalised
 // O^T, row max in the exp2 domain, row sum) to the workspace;
-// prefill_merge_kernel combines the splits of a query tile afterwards.
+// prefill_merge_kernel (hy_paged_prefill_merge) combines the splits of a
+// query tile afterwards.
 
 #include <type_traits>
 
@@ -357,21 +358,25 @@ __global__ __launch_bounds__(512) void prefill_merge_kernel(
 }
 
 template <int G>
-void launch_prefill(hipStream_t st, int num_kv_heads, int n_items, int n_merge,
-                    const uint16_t *q, int64_t q_ss, int64_t q_st, int64_t q_sh, uint16_t *out,
-                    int64_t o_ss, int64_t o_st, int64_t o_sh, const uint16_t *k_pool,
-                    const uint16_t *v_pool, int64_t pool_hs, const int32_t *page_table,
-                    int64_t pt_stride, const int32_t *q_start, const int32_t *kv_lens,
-                    const int32_t *items, const int32_t *merge_items, float *ws_acc,
-                    float *ws_ml, int page_shift, float scale_log2) {
+void launch_prefill(hipStream_t st, int num_kv_heads, int n_items, const uint16_t *q,
+                    int64_t q_ss, int64_t q_st, int64_t q_sh, uint16_t *out, int64_t o_ss,
+                    int64_t o_st, int64_t o_sh, const uint16_t *k_pool, const uint16_t *v_pool,
+                    int64_t pool_hs, const int32_t *page_table, int64_t pt_stride,
+                    const int32_t *q_start, const int32_t *kv_lens, const int32_t *items,
+                    float *ws_acc, float *ws_ml, int page_shift, float scale_log2) {
   hipLaunchKernelGGL(prefill_kernel<G>, dim3(num_kv_heads, n_items), dim3(256), 0, st, q, q_ss,
                      q_st, q_sh, out, o_ss, o_st, o_sh, k_pool, v_pool, pool_hs, page_table,
                      pt_stride, q_start, kv_lens, items, ws_acc, ws_ml, num_kv_heads, page_shift,
                      scale_log2);
-  if (n_merge > 0)
-    hipLaunchKernelGGL(prefill_merge_kernel<G>, dim3(num_kv_heads, n_merge, kRows / 4),
-                       dim3(512), 0, st, out, o_ss, o_st, o_sh, q_start, merge_items, ws_acc,
-                       ws_ml, num_kv_heads);
+}
+
+template <int G>
+void launch_prefill_merge(hipStream_t st, int num_kv_heads, int n_merge, uint16_t *out,
+                          int64_t o_ss, int64_t o_st, int64_t o_sh, const int32_t *q_start,
+                          const int32_t *merge_items, const float *ws_acc, const float *ws_ml) {
+  hipLaunchKernelGGL(prefill_merge_kernel<G>, dim3(num_kv_heads, n_merge, kRows / 4), dim3(512),
+                     0, st, out, o_ss, o_st, o_sh, q_start, merge_items, ws_acc, ws_ml,
+                     num_kv_heads);
 }
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -393,10 +398,9 @@ extern "C" int hy_paged_prefill(
     void *out, int64_t o_stride_seq, int64_t o_stride_tok, int64_t o_stride_head,
     const void *k_pool, const void *v_pool, int64_t pool_head_stride,
     const int32_t *page_table, int64_t page_table_stride, const int32_t *q_start,
-    const int32_t *kv_lens, const int32_t *prefill_items, int32_t n_prefill,
-    const int32_t *merge_items, int32_t n_merge, int32_t n_slots, void *workspace,
-    int64_t workspace_bytes, int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
-    int32_t head_dim, int32_t page_size, float scale, void *stream) {
+    const int32_t *kv_lens, const int32_t *prefill_items, int32_t n_prefill, int32_t n_slots,
+    void *workspace, int64_t workspace_bytes, int32_t num_seqs, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, float scale, void *stream) {
   hy::clear_error();
   HY_REQUIRE(num_seqs >= 1, "num_seqs must be positive");
   HY_REQUIRE(scale > 0.f, "softmax scale must be positive");
@@ -408,13 +412,10 @@ extern "C" int hy_paged_prefill(
                        kHeadDim);
   HY_REQUIRE_SUPPORTED(page_size >= 32 && (page_size & (page_size - 1)) == 0,
                        "page_size %d unsupported (power of two >= 32 required)", page_size);
-  HY_REQUIRE(n_prefill >= 0 && n_merge >= 0 && n_slots >= 0, "item counts must be non-negative");
-  HY_REQUIRE((n_merge == 0) == (n_slots == 0),
-             "n_merge and n_slots must be both zero or both positive");
+  HY_REQUIRE(n_prefill >= 0 && n_slots >= 0, "item counts must be non-negative");
   if (n_prefill == 0) return HY_OK;
   HY_REQUIRE(q && out && k_pool && v_pool && page_table && q_start && kv_lens && prefill_items,
              "hy_paged_prefill: null pointer argument");
-  HY_REQUIRE(n_merge == 0 || merge_items, "merge_items is NULL");
   const int64_t need = hy_prefill_workspace_bytes(n_slots, num_kv_heads, head_dim);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     hy::set_error("workspace too small: need %lld bytes, got %lld",
@@ -438,11 +439,10 @@ extern "C" int hy_paged_prefill(
   const uint16_t *vp = static_cast<const uint16_t *>(v_pool);
 #define HY_PREFILL_CASE(GG)                                                                   \
   case GG:                                                                                    \
-    hy::launch_prefill<GG>(st, num_kv_heads, n_prefill, n_merge, qq, q_stride_seq,            \
-                           q_stride_tok, q_stride_head, oo, o_stride_seq, o_stride_tok,        \
-                           o_stride_head, kp, vp, pool_head_stride, page_table,               \
-                           page_table_stride, q_start, kv_lens, prefill_items, merge_items,   \
-                           ws_acc, ws_ml, page_shift, scale_log2);                            \
+    hy::launch_prefill<GG>(st, num_kv_heads, n_prefill, qq, q_stride_seq, q_stride_tok,       \
+                           q_stride_head, oo, o_stride_seq, o_stride_tok, o_stride_head, kp,  \
+                           vp, pool_head_stride, page_table, page_table_stride, q_start,      \
+                           kv_lens, prefill_items, ws_acc, ws_ml, page_shift, scale_log2);    \
     break;
   switch (G) {
     HY_PREFILL_CASE(1)
@@ -456,4 +456,46 @@ extern "C" int hy_paged_prefill(
   }
 #undef HY_PREFILL_CASE
   return hy::launch_status("hy_paged_prefill");
+}
+
+extern "C" int hy_paged_prefill_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,
+                                      int64_t o_stride_head, const int32_t *q_start,
+                                      const int32_t *merge_items, int32_t n_merge,
+                                      int32_t n_slots, const void *workspace,
+                                      int64_t workspace_bytes, int32_t num_q_heads,
+                                      int32_t num_kv_heads, int32_t head_dim, void *stream) {
+  hy::clear_error();
+  HY_REQUIRE(n_merge >= 0 && n_slots >= 0, "item counts must be non-negative");
+  if (n_merge == 0) return HY_OK;
+  HY_REQUIRE(num_kv_heads >= 1 && num_q_heads >= num_kv_heads &&
+                 num_q_heads % num_kv_heads == 0,
+             "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",
+             num_q_heads, num_kv_heads);
+  HY_REQUIRE_SUPPORTED(head_dim == kHeadDim, "head_dim %d unsupported (need %d)", head_dim,
+                       kHeadDim);
+  HY_REQUIRE(out && q_start && merge_items && workspace,
+             "hy_paged_prefill_merge: null pointer argument");
+  const int64_t need = hy_prefill_workspace_bytes(n_slots, num_kv_heads, head_dim);
+  if (workspace_bytes < need) {
+    hy::set_error("workspace too small: need %lld bytes, got %lld",
+                  static_cast<long long>(need), static_cast<long long>(workspace_bytes));
+    return HY_ENOSPACE;
+  }
+  const int64_t rows = static_cast<int64_t>(n_slots) * num_kv_heads * hy::kRows;
+  const float *ws_acc = static_cast<const float *>(workspace);
+  const float *ws_ml = reinterpret_cast<const float *>(static_cast<const char *>(workspace) +
+                                                       hy::align256(rows * head_dim * 4));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint16_t *oo = static_cast<uint16_t *>(out);
+  switch (num_q_heads / num_kv_heads) {
+    case 1: hy::launch_prefill_merge<1>(st, num_kv_heads, n_merge, oo, o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items, ws_acc, ws_ml); break;
+    case 2: hy::launch_prefill_merge<2>(st, num_kv_heads, n_merge, oo, o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items, ws_acc, ws_ml); break;
+    case 4: hy::launch_prefill_merge<4>(st, num_kv_heads, n_merge, oo, o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items, ws_acc, ws_ml); break;
+    case 8: hy::launch_prefill_merge<8>(st, num_kv_heads, n_merge, oo, o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items, ws_acc, ws_ml); break;
+    case 16: hy::launch_prefill_merge<16>(st, num_kv_heads, n_merge, oo, o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items, ws_acc, ws_ml); break;
+    default:
+      hy::set_error("GQA group size %d unsupported (1, 2, 4, 8, 16)", num_q_heads / num_kv_heads);
+      return HY_EUNSUPPORTED;
+  }
+  return hy::launch_status("hy_paged_prefill_merge");
 }

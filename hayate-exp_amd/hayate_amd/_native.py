@@ -62,15 +62,21 @@ _SIGNATURES = {
     "hy_decode_workspace_bytes": ([_I32, _I32, _I32], ctypes.c_int64),
     "hy_paged_decode": (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64,
-         _P, _P, _I32, _P, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32,
-         _F32, _P],
+         _P, _P, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P],
+        ctypes.c_int,
+    ),
+    "hy_paged_decode_merge": (
+        [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P, _I64, _I32, _I32, _P],
         ctypes.c_int,
     ),
     "hy_prefill_workspace_bytes": ([_I32, _I32, _I32], ctypes.c_int64),
     "hy_paged_prefill": (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64,
-         _P, _P, _P, _I32, _P, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32,
-         _F32, _P],
+         _P, _P, _P, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P],
+        ctypes.c_int,
+    ),
+    "hy_paged_prefill_merge": (
+        [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P, _I64, _I32, _I32, _I32, _P],
         ctypes.c_int,
     ),
 }

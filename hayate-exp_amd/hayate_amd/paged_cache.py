@@ -66,24 +66,31 @@ def _row_strides(t: torch.Tensor, layout: str, q_len: int):
 
     layout "bhtd": (B, H, T, D); "bthd": (B, T, H, D); "thd": packed (N, H, D).
     """
-    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
-        raise ValueError("rows must be contiguous in the last dim and 16-byte aligned")
-    if layout == "bhtd":
-        sb, sh, st, _ = t.stride()
-        return sb - q_len * st, st, sh
-    if layout == "bthd":
-        sb, st, sh, _ = t.stride()
-        return sb - q_len * st, st, sh
+    st = t.stride()
     if layout == "thd":
-        st, sh, _ = t.stride()
-        return 0, st, sh
-    raise ValueError(layout)
+        s_tok, s_head, s_el = st
+        s_seq = 0
+    elif layout == "bhtd":
+        s_b, s_head, s_tok, s_el = st
+        s_seq = s_b - q_len * s_tok
+    elif layout == "bthd":
+        s_b, s_tok, s_head, s_el = st
+        s_seq = s_b - q_len * s_tok
+    else:
+        raise ValueError(layout)
+    if s_el != 1 or (s_tok | s_head | s_seq) & 7 or t.data_ptr() & 15:
+        raise ValueError("rows must be contiguous in the last dim and 16-byte aligned")
+    return s_seq, s_tok, s_head
 
 
 def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
-    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+    st = t.stride()
+    if st[-1] != 1 or t.data_ptr() & 15:
         return t.contiguous()
-    return t
+    acc = 0
+    for x in st[:-1]:
+        acc |= x
+    return t.contiguous() if acc & 7 else t
 
 
 class _DevicePlan:
@@ -120,6 +127,16 @@ class _DevicePlan:
             if self.prefill_workspace_bytes
             else None
         )
+        # raw addresses for the C calls (None for an empty list)
+        def addr(t):
+            return t.data_ptr() if t is not None and t.numel() else None
+
+        self.decode_ptr = addr(self.decode)
+        self.merge_ptr = addr(self.merge)
+        self.prefill_ptr = addr(self.prefill)
+        self.prefill_merge_ptr = addr(self.prefill_merge)
+        self.workspace_ptr = addr(self.workspace)
+        self.prefill_workspace_ptr = addr(self.prefill_workspace)
 
 
 class PagedKVBatch:
@@ -161,6 +178,10 @@ class PagedKVBatch:
         self.query_len = q_lens[0] if not varlen else None
         self.tokens_per_split = tokens_per_split
         self._num_cus = manager.num_cus
+        self._max_kv = max(self.kv_lens_host) if self.kv_lens_host else 0
+        self._pool_ptrs: dict = {}
+        # optional per-kernel timing hook, see _launch
+        self.launch_hook = None
 
         width = max(1, max(len(p) for p in page_lists))
         table = np.full((self.num_seqs, width), -1, dtype=np.int32)
@@ -187,6 +208,11 @@ class PagedKVBatch:
         self.q_start = meta[n + 2 * b : n + 3 * b + 1]
         self.cache_lens = self.cache_lens_i32.to(torch.long)
         self._meta = meta
+        self._pt_ptr = self.page_table.data_ptr()
+        self._pt_stride = self.page_table.stride(0)
+        self._q_start_ptr = self.q_start.data_ptr()
+        self._cache_lens_ptr = self.cache_lens_i32.data_ptr()
+        self._kv_lens_ptr = self.kv_lens.data_ptr()
         self._plans: dict[int, tuple] = {}
         if num_q_heads is not None and self.device.type == "cuda":
             self.plan(num_q_heads)
@@ -211,9 +237,23 @@ class PagedKVBatch:
         return plan
 
     def _layer_pools(self, layer_idx: int):
-        k_layer = self.k_cache[layer_idx, 0]
-        v_layer = self.v_cache[layer_idx, 0]
-        return k_layer, v_layer, k_layer.stride(0)
+        """(k_ptr, v_ptr, head_stride) of one layer's pool slice, cached
+        per batch (the pool tensors outlive the batch)."""
+        hit = self._pool_ptrs.get(layer_idx)
+        if hit is not None:
+            return hit
+        num_layers = self.k_cache.shape[0]
+        if not -num_layers <= layer_idx < num_layers:
+            raise IndexError(f"layer {layer_idx} out of range for {num_layers} layers")
+        layer = layer_idx % num_layers
+        el = self.k_cache.element_size()
+        hit = (
+            self.k_cache.data_ptr() + layer * self.k_cache.stride(0) * el,
+            self.v_cache.data_ptr() + layer * self.v_cache.stride(0) * el,
+            self.k_cache.stride(2),
+        )
+        self._pool_ptrs[layer_idx] = hit
+        return hit
 
     def _layout(self, t: torch.Tensor, uniform_layout: str) -> tuple:
         if self.varlen:
@@ -235,14 +275,13 @@ class PagedKVBatch:
         k = _aligned_rows(k)
         v = _aligned_rows(v)
         self._check_kv(k, v, head_axis=1)
-        k_layer, v_layer, hs = self._layer_pools(layer_idx)
+        k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
         ks = self._layout(k, "bhtd")
         vs = self._layout(v, "bhtd")
         rc = _native.lib().hy_kv_append(
-            k_layer.data_ptr(), v_layer.data_ptr(), hs,
+            k_ptr, v_ptr, hs,
             k.data_ptr(), *ks, v.data_ptr(), *vs,
-            self.q_start.data_ptr(), self.cache_lens_i32.data_ptr(),
-            self.page_table.data_ptr(), self.page_table.stride(0),
+            self._q_start_ptr, self._cache_lens_ptr, self._pt_ptr, self._pt_stride,
             self.num_seqs, self.total_tokens, self.num_kv_heads, self.head_dim,
             self.page_size, _stream_handle(self.device),
         )
@@ -284,9 +323,9 @@ class PagedKVBatch:
             cos = cos.contiguous()
             sin = sin.contiguous()
             max_pos = cos.shape[0]
-            if max(self.kv_lens_host) > max_pos:
+            if self._max_kv > max_pos:
                 raise ValueError(
-                    f"positions up to {max(self.kv_lens_host) - 1} exceed the rope "
+                    f"positions up to {self._max_kv - 1} exceed the rope "
                     f"table ({max_pos} positions)"
                 )
         else:
@@ -296,7 +335,7 @@ class PagedKVBatch:
         for w in (qw, kw):
             if w is not None and (w.dtype != torch.bfloat16 or w.numel() != self.head_dim):
                 raise TypeError("norm weights must be bfloat16 (head_dim,)")
-        k_layer, v_layer, hs = self._layer_pools(layer_idx)
+        k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
         rc = _native.lib().hy_qknorm_rope_append(
             q.data_ptr(), *qs, q_out.data_ptr(), *qos,
             k.data_ptr(), *ks, v.data_ptr(), *vs,
@@ -304,9 +343,8 @@ class PagedKVBatch:
             None if kw is None else kw.data_ptr(), float(eps),
             None if cos is None else cos.data_ptr(),
             None if sin is None else sin.data_ptr(), max_pos,
-            k_layer.data_ptr(), v_layer.data_ptr(), hs,
-            self.q_start.data_ptr(), self.cache_lens_i32.data_ptr(),
-            self.page_table.data_ptr(), self.page_table.stride(0),
+            k_ptr, v_ptr, hs,
+            self._q_start_ptr, self._cache_lens_ptr, self._pt_ptr, self._pt_stride,
             self.num_seqs, self.total_tokens, num_q_heads, self.num_kv_heads,
             self.head_dim, self.page_size, _stream_handle(self.device),
         )
@@ -326,6 +364,20 @@ class PagedKVBatch:
             raise ValueError("k/v head count does not match the pool")
 
     # ---------------------------------------------------------- attend path
+    def _launch(self, name: str, fn, *args) -> None:
+        """Enqueues one C-ABI call. A `launch_hook(name, after)` set on the
+        batch is called right before (after=False) and right after
+        (after=True) the call, so a caller can bracket one kernel with
+        events on the launch stream."""
+        hook = self.launch_hook
+        if hook is not None:
+            hook(name, False)
+        rc = fn(*args)
+        if rc:
+            _native.check(rc, name)
+        if hook is not None:
+            hook(name, True)
+
     def attend_layer(
         self, q: torch.Tensor, layer_idx: int, scale: Optional[float] = None
     ) -> torch.Tensor:
@@ -359,36 +411,42 @@ class PagedKVBatch:
         if scale is None:
             scale = 1.0 / math.sqrt(self.head_dim)
         plan = self.plan(num_q_heads)
-        k_layer, v_layer, hs = self._layer_pools(layer_idx)
+        k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
         stream = _stream_handle(self.device)
+        lib = _native.lib()
         if plan.n_decode:
-            rc = _native.lib().hy_paged_decode(
+            self._launch("hy_paged_decode", lib.hy_paged_decode,
                 q.data_ptr(), *qs, result.data_ptr(), *os_,
-                k_layer.data_ptr(), v_layer.data_ptr(), hs,
-                self.page_table.data_ptr(), self.page_table.stride(0),
-                self.q_start.data_ptr(), plan.decode.data_ptr(), plan.n_decode,
-                plan.merge.data_ptr() if plan.n_merge else None, plan.n_merge, plan.n_slots,
-                None if plan.workspace is None else plan.workspace.data_ptr(),
-                plan.workspace_bytes, self.num_seqs, num_q_heads,
+                k_ptr, v_ptr, hs,
+                self._pt_ptr, self._pt_stride, self._q_start_ptr, plan.decode_ptr,
+                plan.n_decode, plan.n_slots, plan.workspace_ptr, plan.workspace_bytes, self.num_seqs, num_q_heads,
                 self.num_kv_heads, self.head_dim, self.page_size, float(scale),
                 stream,
             )
-            _native.check(rc, "hy_paged_decode")
+        if plan.n_merge:
+            self._launch("hy_paged_decode_merge", lib.hy_paged_decode_merge,
+                result.data_ptr(), *os_, self._q_start_ptr,
+                plan.merge_ptr, plan.n_merge, plan.n_slots,
+                plan.workspace_ptr, plan.workspace_bytes, num_q_heads,
+                self.head_dim, stream,
+            )
         if plan.n_prefill:
-            rc = _native.lib().hy_paged_prefill(
+            self._launch("hy_paged_prefill", lib.hy_paged_prefill,
                 q.data_ptr(), *qs, result.data_ptr(), *os_,
-                k_layer.data_ptr(), v_layer.data_ptr(), hs,
-                self.page_table.data_ptr(), self.page_table.stride(0),
-                self.q_start.data_ptr(), self.kv_lens.data_ptr(),
-                plan.prefill.data_ptr(), plan.n_prefill,
-                plan.prefill_merge.data_ptr() if plan.n_prefill_merge else None,
-                plan.n_prefill_merge, plan.n_prefill_slots,
-                None if plan.prefill_workspace is None else plan.prefill_workspace.data_ptr(),
-                plan.prefill_workspace_bytes, self.num_seqs, num_q_heads,
+                k_ptr, v_ptr, hs,
+                self._pt_ptr, self._pt_stride, self._q_start_ptr, self._kv_lens_ptr,
+                plan.prefill_ptr, plan.n_prefill, plan.n_prefill_slots,
+                plan.prefill_workspace_ptr, plan.prefill_workspace_bytes, self.num_seqs, num_q_heads,
                 self.num_kv_heads, self.head_dim, self.page_size, float(scale),
                 stream,
             )
-            _native.check(rc, "hy_paged_prefill")
+        if plan.n_prefill_merge:
+            self._launch("hy_paged_prefill_merge", lib.hy_paged_prefill_merge,
+                result.data_ptr(), *os_, self._q_start_ptr,
+                plan.prefill_merge_ptr, plan.n_prefill_merge, plan.n_prefill_slots,
+                plan.prefill_workspace_ptr, plan.prefill_workspace_bytes,
+                num_q_heads, self.num_kv_heads, self.head_dim, stream,
+            )
         return result
 
 

@@ -84,9 +84,11 @@ class Workload:
         return self.batch
 
     # Algorithmic work of one step (numerators of the roofline fractions).
-    def decode_bytes(self) -> int:
+    def decode_bytes(self, include_append: bool = True) -> int:
         """HBM bytes a decode step must move: every K/V row of every decode
-        context once (shared pages once), q and output rows, appended rows."""
+        context once (shared pages once), q and output rows and, with
+        include_append, the appended K/V rows (written by the append
+        kernel, not by attention)."""
         seen = set()
         tokens = 0
         n_dec = 0
@@ -102,7 +104,7 @@ class Workload:
                 seen.add(pages[j])
                 tokens += used
         qo = n_dec * 2 * NUM_Q_HEADS * HEAD_DIM * 2
-        append = n_dec * KV_BYTES_PER_TOKEN
+        append = n_dec * KV_BYTES_PER_TOKEN if include_append else 0
         return tokens * KV_BYTES_PER_TOKEN + qo + append
 
     def prefill_pairs(self) -> int:

@@ -158,9 +158,10 @@ int64_t hy_decode_workspace_bytes(int32_t n_slots, int32_t num_q_heads,
  * Paged GQA decode attention for sequences with one query token each
  * (items from hy_plan_tick). Each workgroup covers one decode item and one
  * kv head, loads every K/V row of its token range once and applies it to
- * all num_q_heads / num_kv_heads query heads (QK^T and PV on MFMA). When
- * n_merge > 0 a second launch on the same stream merges the fp32 partials
- * of split sequences (log-sum-exp) into the output.
+ * all num_q_heads / num_kv_heads query heads (QK^T and PV on MFMA).
+ * Sequences with several splits leave fp32 partials in the workspace;
+ * hy_paged_decode_merge, enqueued after this call on the same stream,
+ * completes them.
  * Causal semantics: the query of sequence b at position kv_len - 1 sees
  * every key k < kv_len (paged_cache.py:266-271).
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T == 1.
@@ -172,11 +173,22 @@ int hy_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
                     int64_t pool_head_stride, const int32_t *page_table,
                     int64_t page_table_stride, const int32_t *q_start,
                     const int32_t *decode_items, int32_t n_decode,
-                    const int32_t *merge_items, int32_t n_merge,
                     int32_t n_slots, void *workspace, int64_t workspace_bytes,
                     int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t page_size, float scale,
                     void *stream);
+
+/*
+ * Merge of split decode partials (log-sum-exp over the splits of each
+ * merge item) into the bf16 output rows of hy_paged_decode. Second half of
+ * PagedKVBatch.attend_layer (paged_cache.py:62-71) for split sequences.
+ */
+int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,
+                          int64_t o_stride_head, const int32_t *q_start,
+                          const int32_t *merge_items, int32_t n_merge,
+                          int32_t n_slots, const void *workspace,
+                          int64_t workspace_bytes, int32_t num_q_heads,
+                          int32_t head_dim, void *stream);
 
 /* Prefill split workspace bytes for n_slots partials (fp32 acc[head_dim],
  * max, sum for each of the 256 rows of a query tile, per kv head). */
@@ -187,8 +199,9 @@ int64_t hy_prefill_workspace_bytes(int32_t n_slots, int32_t num_kv_heads,
  * Paged chunked-prefill causal attention (bf16 MFMA) for sequences with
  * q_len > 1 (prefill items from hy_plan_tick): query i of sequence b at
  * logical position cache_len_b + i sees every cached prefix key and the
- * chunk's keys up to itself. K/V are read through the page table. When
- * n_merge > 0 a second launch on the same stream merges the splits.
+ * chunk's keys up to itself. K/V are read through the page table. Split
+ * query tiles leave fp32 partials in the workspace; hy_paged_prefill_merge,
+ * enqueued after this call on the same stream, completes them.
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T > 1.
  */
 int hy_paged_prefill(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
@@ -198,12 +211,23 @@ int hy_paged_prefill(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
                      int64_t pool_head_stride, const int32_t *page_table,
                      int64_t page_table_stride, const int32_t *q_start,
                      const int32_t *kv_lens, const int32_t *prefill_items,
-                     int32_t n_prefill, const int32_t *merge_items,
-                     int32_t n_merge, int32_t n_slots, void *workspace,
+                     int32_t n_prefill, int32_t n_slots, void *workspace,
                      int64_t workspace_bytes, int32_t num_seqs,
                      int32_t num_q_heads, int32_t num_kv_heads,
                      int32_t head_dim, int32_t page_size, float scale,
                      void *stream);
+
+/*
+ * Merge of split prefill partials into the bf16 output rows of
+ * hy_paged_prefill (one merge item per split query tile).
+ */
+int hy_paged_prefill_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,
+                           int64_t o_stride_head, const int32_t *q_start,
+                           const int32_t *merge_items, int32_t n_merge,
+                           int32_t n_slots, const void *workspace,
+                           int64_t workspace_bytes, int32_t num_q_heads,
+                           int32_t num_kv_heads, int32_t head_dim,
+                           void *stream);
 
 #ifdef __cplusplus
 }

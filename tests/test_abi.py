@@ -133,16 +133,28 @@ def test_entry_points_validate_before_touching_the_device():
     assert rc == _native.HY_EUNSUPPORTED
     # GQA group 3 is not built
     rc = lib.hy_paged_decode(fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, 0, fake, 0, fake,
-                             fake, 1, None, 0, 0, None, 0, 1, 6, 2, 128, 128, 0.1, None)
+                             fake, 1, 0, None, 0, 1, 6, 2, 128, 128, 0.1, None)
     assert rc == _native.HY_EUNSUPPORTED
     # workspace too small for the slots
     rc = lib.hy_paged_decode(fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, 0, fake, 0, fake,
-                             fake, 2, fake, 1, 2, fake, 100, 1, 32, 8, 128, 128, 0.1, None)
+                             fake, 2, 2, fake, 100, 1, 32, 8, 128, 128, 0.1, None)
     assert rc == _native.HY_ENOSPACE
     with pytest.raises(MemoryError):
         _native.check(rc, "hy_paged_decode")
+    rc = lib.hy_paged_decode_merge(fake, 0, 0, 0, fake, fake, 1, 2, fake, 100, 32, 128, None)
+    assert rc == _native.HY_ENOSPACE
+    rc = lib.hy_paged_prefill_merge(fake, 0, 0, 0, fake, fake, 1, 2, fake, 100, 32, 8, 128,
+                                    None)
+    assert rc == _native.HY_ENOSPACE
+    rc = lib.hy_paged_prefill_merge(fake, 0, 0, 0, fake, fake, 1, 2, fake, 1 << 30, 24, 8, 128,
+                                    None)
+    assert rc == _native.HY_EUNSUPPORTED
     # nothing to do is success, even with null buffers
     assert lib.hy_paged_prefill(None, 0, 0, 0, None, 0, 0, 0, None, None, 0, None, 0, None,
-                                None, None, 0, None, 0, 0, None, 0, 1, 32, 8, 128, 128, 0.1,
+                                None, None, 0, 0, None, 0, 1, 32, 8, 128, 128, 0.1,
                                 None) == 0
+    assert lib.hy_paged_decode_merge(None, 0, 0, 0, None, None, 0, 0, None, 0, 32, 128,
+                                     None) == 0
+    assert lib.hy_paged_prefill_merge(None, 0, 0, 0, None, None, 0, 0, None, 0, 32, 8, 128,
+                                      None) == 0
     assert lib.hy_last_error() == b""
