@@ -1,10 +1,18 @@
 // Paged chunked-prefill causal attention on bf16 MFMA (gfx950).
 //
-// Grid: (kv head, prefill item); heads vary fastest so that the dispatcher
-// walks items in the planner's longest-first order. An item is a tile of
-// 256 / G query tokens of one sequence, with its G query heads 256
-// (token, head) rows that all read the same K/V (GQA), over the key range
-// [kv_begin, kv_end) of one split. Four waves of 64 rows (two 32-row blocks).
+// Grid: (kv head, prefill item); heads vary fastest, so the dispatcher walks
+// items in the planner's longest-first order and, with 8 kv heads on the 8
+// XCDs, every workgroup of one kv head lands on the same XCD (its L2 holds
+// that head's K/V pages for all query tiles of the request). An item is a
+// tile of 256 / G query tokens of one sequence; with its G query heads that
+// is 256 (token, head) rows, all reading the same K/V rows (GQA), over the
+// key range [kv_begin, kv_end) of one split.
+//
+// Eight waves of 32 rows, two waves per SIMD: while one wave of a SIMD runs
+// its softmax on the VALU the other one keeps the matrix core busy (a wave
+// cannot overlap its own exp/fma work with its MFMAs). Row r = 32 w + c is
+// token q_begin + r / G, head kv_head * G + r % G, so a wave spans 32 / G
+// consecutive tokens and the causal diagonal cuts few of its key blocks.
 //
 // v_mfma_f32_32x32x16_bf16, transposed formulation (lane l, c = l % 32,
 // h = l / 32):
@@ -12,19 +20,20 @@
 //                 lane, 272-byte rows: conflict-free); B = Q^T held in
 //                 registers. Lane (c, h) ends with row c's scores for keys
 //                 8 (i / 4) + 4 h + i % 4, i < 16, of the 32-key block.
-//   softmax       per row: the two lanes of a row differ only in h (xor 32).
+//   softmax       per row: the two lanes of a row differ only in h; the
+//                 row max and sum cross halves with v_permlane32_swap.
 //   O^T += V^T P^T  B = P^T: the first (last) eight of the lane's scores
 //                 are row c's probabilities for MFMA k index 8 h + j once k
 //                 stands for key 16 kh + (j < 4 ? 4 h + j : 8 + 4 h + j - 4);
 //                 A = V^T from LDS with ds_read_b64_tr_b16 (288-byte rows,
 //                 conflict-free), which hands lane r of a 16-lane group four
 //                 consecutive keys of dim r.
-// Two row blocks per wave share every K and V operand read, halving LDS
-// traffic per flop. K/V tiles of 64 keys are double buffered in LDS; the
-// next tile is loaded into registers while the current one is computed.
-// The softmax rescales lazily: the exponent base of a row only moves when
-// its max grows by more than 2^8, so the accumulators (held in AGPRs) are
-// rarely touched by VALU.
+// K/V tiles of KEYS keys are double buffered in LDS: the next tile is loaded
+// into registers while the current one is computed, then stored, then one
+// barrier. The softmax rescales lazily: the exponent base of a row only
+// moves when its max grows by more than 2^8, so the accumulators are rarely
+// touched by VALU. Key blocks past the causal limit of every row of a wave
+// are skipped by that wave.
 // Rows at or past kv_end are filled from the last valid key, so masked
 // scores never meet NaN bits of unwritten rows.
 //
@@ -32,6 +41,10 @@
 // O^T, row max in the exp2 domain, row sum) to the workspace;
 // prefill_merge_kernel (hy_paged_prefill_merge) combines the splits of a
 // query tile afterwards.
+//
+// Item key ranges start at multiples of 32 keys (hy_plan_tick cuts at
+// multiples of the tile size), so each 32-key row group of a tile lies in
+// one page and its page-table entry is a scalar load.
 
 #include <type_traits>
 
@@ -41,11 +54,12 @@ namespace hy {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kRows = 256;   // (token, head) rows per workgroup
-constexpr int kKeys = 64;    // keys per LDS stage
-constexpr int kKRow = 136;   // u16 per K row in LDS (272 bytes)
-constexpr int kVRow = 144;   // u16 per V row in LDS (288 bytes)
+constexpr int kRows = 256;     // (token, head) rows per workgroup
+constexpr int kThreads = 512;  // eight waves of 32 rows
+constexpr int kKRow = 136;     // u16 per K row in LDS (272 bytes)
+constexpr int kVRow = 144;     // u16 per V row in LDS (288 bytes)
 constexpr float kLazy = 8.0f;  // rescale threshold, exp2 domain
+constexpr int kTileKeys = 64;  // keys per LDS stage: two 32-key blocks
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -62,8 +76,22 @@ __device__ __forceinline__ s16x4 tr_read(const uint16_t *p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(const_cast<uint16_t *>(p)));
 }
 
-template <int G>
-__global__ __launch_bounds__(256) void prefill_kernel(
+// v_permlane32_swap with both operands x: the first result holds, in every
+// lane, x of lane l % 32 and the second x of lane 32 + l % 32, so combining
+// the two gives the same value in both lanes of a row.
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int G, int KEYS>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
     uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
@@ -71,8 +99,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ kv_lens,
     const int32_t *__restrict__ items, float *__restrict__ ws_acc, float *__restrict__ ws_ml,
     int num_kv_heads, int page_shift, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kKeys * kKRow];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kKeys * kVRow];
+  static_assert(KEYS % 32 == 0 && KEYS >= 32, "tiles are whole 32-key blocks");
+  constexpr int kChunks = KEYS / 32;  // 16-byte K (and V) chunks per thread per tile
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][KEYS * kKRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][KEYS * kVRow];
 
   const int32_t *it = items + 8 * blockIdx.y;
   const int kvh = blockIdx.x;
@@ -93,68 +123,71 @@ __global__ __launch_bounds__(256) void prefill_kernel(
   const int c = lane & 31;
   const int h = lane >> 5;
 
-  // Q^T operand of both row blocks: row r = 64 wave + 32 rb + c.
-  bf16x8 qop[2][8];
-  int row_tok[2];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int r = 64 * wave + 32 * rb + c;
-    const int i = q_begin + r / G;
-    row_tok[rb] = i;
-    const bool live = i < q_end;
-    const uint16_t *src = q + seq * q_ss + static_cast<int64_t>(qs + (live ? i : q_begin)) * q_st +
+  // This lane's row and its Q^T operand (zeros for rows past the chunk).
+  const int r = 32 * wave + c;
+  const int row_tok = q_begin + r / G;
+  const bool live = row_tok < q_end;
+  bf16x8 qop[8];
+  {
+    const uint16_t *src = q + seq * q_ss +
+                          static_cast<int64_t>(qs + (live ? row_tok : q_begin)) * q_st +
                           (h0 + r % G) * q_sh;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
       u32x4 w = {0u, 0u, 0u, 0u};
       if (live) w = load16(src + 16 * kk + 8 * h);
-      qop[rb][kk] = __builtin_bit_cast(bf16x8, w);
+      qop[kk] = __builtin_bit_cast(bf16x8, w);
     }
   }
 
-  f32x16 acc[2][4];
+  f32x16 acc[4];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[rb][db][i] = 0.f;
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
+    for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  // Causal limits: this row sees keys <= limit; every live row of the wave
+  // sees keys <= wave_lo; no live row of the wave sees a key > wave_hi.
+  const int last_key = kv_end - 1;
+  const int limit = min(cache_len + row_tok, last_key);
+  const int tw0 = q_begin + (32 * wave) / G;
+  const int tw1 = min(q_end - 1, q_begin + (32 * wave + 31) / G);
+  const bool wave_live = tw0 < q_end;
+  const int wave_lo = min(cache_len + tw0, last_key);
+  const int wave_hi = min(cache_len + tw1, last_key);
 
   const uint16_t *kh = k_pool + kvh * pool_hs;
   const uint16_t *vh = v_pool + kvh * pool_hs;
   const int32_t *pt = page_table + seq * pt_stride;
   const int page_mask = (1 << page_shift) - 1;
-  const int diag_begin = cache_len + q_begin;  // first key masked for some row
 
-  // Staging: thread t moves 16-byte chunks j * 256 + t of the K and V tiles
-  // (row = chunk / 16, dims 8 (chunk % 16) .. +7). A tile starts at a
-  // multiple of 64 keys, so rows 0-31 and 32-63 each lie in one page: two
-  // wave-uniform (scalar) page lookups per tile. Rows at or past kv_end
+  // Staging: thread t moves chunk j < kChunks of the K and of the V tile:
+  // row 32 j + t / 16, dims 8 (t % 16) .. +7. Row group j (32 rows) lies in
+  // one page: one wave-uniform page lookup per group. Rows at or past kv_end
   // read the last valid key instead (any finite data: their scores are
-  // masked), so the loads need no branch and the stores no select.
-  auto load_tile = [&](int kt, u32x4(&kr)[4], u32x4(&vr)[4]) __attribute__((always_inline)) {
-    const int last = kv_end - 1;
-    const int64_t page_lo = pt[kt >> page_shift];
-    const int64_t page_hi = pt[min(kt + 32, last) >> page_shift];
+  // masked), so the loads need no branch.
+  const int srow = tid >> 4;
+  const int scol = (tid & 15) * 8;
+  auto load_tile = [&](int kt, u32x4(&kr)[kChunks], u32x4(&vr)[kChunks])
+                       __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int ch = tid + 256 * j;
-      const int row = ch >> 4;
-      const int key = min(kt + row, last);
-      const int64_t p = ((row < 32 ? page_lo : page_hi) << page_shift) + (key & page_mask);
-      kr[j] = load16(kh + p * kHeadDim + (ch & 15) * 8);
-      vr[j] = load16(vh + p * kHeadDim + (ch & 15) * 8);
+    for (int j = 0; j < kChunks; ++j) {
+      const int g0 = min(kt + 32 * j, last_key);
+      const int64_t page = pt[g0 >> page_shift];
+      const int key = min(kt + 32 * j + srow, last_key);
+      const int64_t p = (page << page_shift) + (key & page_mask);
+      kr[j] = load16(kh + p * kHeadDim + scol);
+      vr[j] = load16(vh + p * kHeadDim + scol);
     }
   };
-  auto store_tile = [&](int b, const u32x4(&kr)[4], const u32x4(&vr)[4])
+  auto store_tile = [&](int b, const u32x4(&kr)[kChunks], const u32x4(&vr)[kChunks])
                         __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int ch = tid + 256 * j;
-      *reinterpret_cast<u32x4 *>(&sK[b][(ch >> 4) * kKRow + (ch & 15) * 8]) = kr[j];
-      *reinterpret_cast<u32x4 *>(&sV[b][(ch >> 4) * kVRow + (ch & 15) * 8]) = vr[j];
+    for (int j = 0; j < kChunks; ++j) {
+      *reinterpret_cast<u32x4 *>(&sK[b][(32 * j + srow) * kKRow + scol]) = kr[j];
+      *reinterpret_cast<u32x4 *>(&sV[b][(32 * j + srow) * kVRow + scol]) = vr[j];
     }
   };
 
@@ -164,113 +197,105 @@ __global__ __launch_bounds__(256) void prefill_kernel(
   const int q16 = lane >> 4;
   const int k_base = c * kKRow + 8 * h;
   const int v_base = (4 * (q16 >> 1) + (r16 >> 2)) * kVRow + 16 * (q16 & 1) + 4 * (r16 & 3);
+  const float lazy_raw = kLazy / scale_log2;  // kLazy in raw score units
+
+  // One 32-key block starting at key kb0, K/V rows at Kb/Vb in LDS.
+  auto block = [&](auto masked, const uint16_t *Kb, const uint16_t *Vb, int kb0)
+                   __attribute__((always_inline)) {
+    constexpr bool kMasked = decltype(masked)::value;
+    f32x16 s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const bf16x8 kop = *reinterpret_cast<const bf16x8 *>(Kb + k_base + 16 * kk);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[kk], s, 0, 0, 0);
+    }
+    if constexpr (kMasked) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (key > limit) s[i] = -INFINITY;
+      }
+    }
+    float m = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int i = 2; i < 16; ++i) m = fmaxf(m, s[i]);
+    m = halves_max(m);
+    // m_run is the exponent base; it only moves when the row max exceeds it
+    // by more than kLazy in the exp2 domain (from -inf: at the first
+    // visible key), so probabilities stay below 2^kLazy.
+    if (__builtin_expect(__any(m > m_run + lazy_raw), 0)) {
+      const float m_new = fmaxf(m_run, m);
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+    }
+    // A row whose keys are all masked so far keeps m = -inf: base 0 gives zeros.
+    const float mc = m_run == -INFINITY ? 0.f : m_run * scale_log2;
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], scale_log2, -mc));
+      s[i] = p;
+      psum += p;
+    }
+    l_run += psum;
+    const bf16x8 pop0 = pack8(s, 0);
+    const bf16x8 pop1 = pack8(s, 8);
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int kh2 = 0; kh2 < 2; ++kh2) {
+        const uint16_t *vp = Vb + v_base + 16 * kh2 * kVRow + 32 * db;
+        const s16x4 lo = tr_read(vp);
+        const s16x4 hi = tr_read(vp + 8 * kVRow);
+        const s16x8 v8 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, v8),
+                                                          kh2 ? pop1 : pop0, acc[db], 0, 0, 0);
+      }
+  };
 
   {
-    u32x4 kr[4], vr[4];
+    u32x4 kr[kChunks], vr[kChunks];
     load_tile(kv_begin, kr, vr);
     store_tile(0, kr, vr);
   }
   __syncthreads();
 
-  // m_run is the max used as the exponent base; it only moves when a row
-  // max exceeds it by more than kLazy in the exp2 domain, so probabilities
-  // stay below 2^kLazy and the accumulators are rescaled rarely.
-  auto step = [&](auto masked, const uint16_t *Kb, const uint16_t *Vb, int kt)
-                  __attribute__((always_inline)) {
-    constexpr bool kMasked = decltype(masked)::value;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      f32x16 s[2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[rb][i] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8 kop =
-            *reinterpret_cast<const bf16x8 *>(Kb + k_base + 32 * kb * kKRow + 16 * kk);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-          s[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[rb][kk], s[rb], 0, 0, 0);
-      }
-
-      float mloc[2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        if constexpr (kMasked) {
-          const int limit = cache_len + row_tok[rb];  // last visible key of this row
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kt + 32 * kb + 8 * (i >> 2) + 4 * h + (i & 3);
-            if (key > limit) s[rb][i] = -INFINITY;
-          }
-        }
-        float m = s[rb][0];
-#pragma unroll
-        for (int i = 1; i < 16; ++i) m = fmaxf(m, s[rb][i]);
-        mloc[rb] = fmaxf(m, __shfl_xor(m, 32));
-      }
-      if (__any(mloc[0] * scale_log2 > m_run[0] * scale_log2 + kLazy ||
-                mloc[1] * scale_log2 > m_run[1] * scale_log2 + kLazy)) {
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-          const float m_new = fmaxf(m_run[rb], mloc[rb]);
-          const float alpha = m_new == -INFINITY
-                                  ? 1.f
-                                  : __builtin_amdgcn_exp2f((m_run[rb] - m_new) * scale_log2);
-          m_run[rb] = m_new;
-          l_run[rb] *= alpha;
-#pragma unroll
-          for (int db = 0; db < 4; ++db) acc[rb][db] *= alpha;
-        }
-      }
-
-      bf16x8 pop[2][2];  // [rb][kh]
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        // A row with every key so far masked keeps m = -inf: base 0 gives zeros.
-        const float mc = m_run[rb] == -INFINITY ? 0.f : m_run[rb] * scale_log2;
-        float psum = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][i], scale_log2, -mc));
-          s[rb][i] = p;
-          psum += p;
-        }
-        pop[rb][0] = pack8(s[rb], 0);
-        pop[rb][1] = pack8(s[rb], 8);
-        l_run[rb] += psum;
-      }
-
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int kh2 = 0; kh2 < 2; ++kh2) {
-          const uint16_t *vp = Vb + v_base + (32 * kb + 16 * kh2) * kVRow + 32 * db;
-          const s16x4 lo = tr_read(vp);
-          const s16x4 hi = tr_read(vp + 8 * kVRow);
-          const s16x8 v8 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb)
-            acc[rb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8, v8), pop[rb][kh2], acc[rb][db], 0, 0, 0);
-        }
-    }
-  };
-
-  // Tiles wholly below the diagonal need no mask; the rest (the diagonal
-  // tiles of the query chunk, always last) do. Two loops keep the two bodies
-  // apart (a per-tile choice between them doubles register pressure).
-  const int n_tiles = (kv_end - kv_begin + kKeys - 1) / kKeys;
-  int n_plain = (diag_begin - kv_begin) / kKeys;  // tiles ending at or before diag_begin
+  // Tiles whose keys every live row of the workgroup sees need no mask
+  // (they come first); the rest decide per wave and 32-key block whether to
+  // skip, compute plainly or mask.
+  const int n_tiles = (kv_end - kv_begin + KEYS - 1) / KEYS;
+  int n_plain = (min(cache_len + q_begin, last_key) + 1 - kv_begin) / KEYS;
   n_plain = n_plain < 0 ? 0 : (n_plain > n_tiles ? n_tiles : n_plain);
-  auto iterate = [&](auto masked, int t) __attribute__((always_inline)) {
-    const int kt = kv_begin + kKeys * t;
+  auto iterate = [&](auto diag, int t) __attribute__((always_inline)) {
+    constexpr bool kDiag = decltype(diag)::value;
+    const int kt = kv_begin + KEYS * t;
     const int b = t & 1;
     const bool has_next = t + 1 < n_tiles;
-    u32x4 kr[4], vr[4];
-    if (has_next) load_tile(kt + kKeys, kr, vr);
-    step(masked, sK[b], sV[b], kt);
+    u32x4 kr[kChunks], vr[kChunks];
+    if (has_next) load_tile(kt + KEYS, kr, vr);
+    if (wave_live) {
+#pragma unroll
+      for (int kb = 0; kb < KEYS / 32; ++kb) {
+        const uint16_t *Kb = sK[b] + 32 * kb * kKRow;
+        const uint16_t *Vb = sV[b] + 32 * kb * kVRow;
+        const int kb0 = kt + 32 * kb;
+        if constexpr (!kDiag) {
+          block(std::false_type{}, Kb, Vb, kb0);
+        } else {
+          if (kb0 <= wave_hi) {
+            if (kb0 + 31 <= wave_lo)
+              block(std::false_type{}, Kb, Vb, kb0);
+            else
+              block(std::true_type{}, Kb, Vb, kb0);
+          }
+        }
+      }
+    }
     if (has_next) {
       store_tile(b ^ 1, kr, vr);
       __syncthreads();
@@ -280,43 +305,37 @@ __global__ __launch_bounds__(256) void prefill_kernel(
   for (int t = n_plain; t < n_tiles; ++t) iterate(std::true_type{}, t);
 
   // Epilogue: full row sums, then the output or the split's partial.
+  const float lsum = halves_sum(l_run);
+  if (slot < 0) {
+    if (!live) return;
+    const float inv = 1.0f / lsum;
+    uint16_t *dst = out + seq * o_ss + static_cast<int64_t>(qs + row_tok) * o_st +
+                    (h0 + r % G) * o_sh;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const float lsum = l_run[rb] + __shfl_xor(l_run[rb], 32);
-    const int r = 64 * wave + 32 * rb + c;
-    if (slot < 0) {
-      const int i = row_tok[rb];
-      if (i >= q_end) continue;
-      const float inv = 1.0f / lsum;
-      uint16_t *dst =
-          out + seq * o_ss + static_cast<int64_t>(qs + i) * o_st + (h0 + r % G) * o_sh;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const int d = 32 * db + 8 * i4 + 4 * h;
-          const uint32_t w0 = f32_to_bf16_rne(acc[rb][db][4 * i4] * inv) |
-                              (f32_to_bf16_rne(acc[rb][db][4 * i4 + 1] * inv) << 16);
-          const uint32_t w1 = f32_to_bf16_rne(acc[rb][db][4 * i4 + 2] * inv) |
-                              (f32_to_bf16_rne(acc[rb][db][4 * i4 + 3] * inv) << 16);
-          *reinterpret_cast<uint2 *>(dst + d) = make_uint2(w0, w1);
-        }
-    } else {
-      const int64_t pr = (static_cast<int64_t>(slot) * num_kv_heads + kvh) * kRows + r;
-      float *dst = ws_acc + pr * kHeadDim;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const int d = 32 * db + 8 * i4 + 4 * h;
-          *reinterpret_cast<f32x4 *>(dst + d) =
-              f32x4{acc[rb][db][4 * i4], acc[rb][db][4 * i4 + 1], acc[rb][db][4 * i4 + 2],
-                    acc[rb][db][4 * i4 + 3]};
-        }
-      if (h == 0) {
-        ws_ml[pr * 2 + 0] = m_run[rb] == -INFINITY ? -INFINITY : m_run[rb] * scale_log2;
-        ws_ml[pr * 2 + 1] = lsum;
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int d = 32 * db + 8 * i4 + 4 * h;
+        const uint32_t w0 = pack_bf16x2_rne(acc[db][4 * i4] * inv, acc[db][4 * i4 + 1] * inv);
+        const uint32_t w1 =
+            pack_bf16x2_rne(acc[db][4 * i4 + 2] * inv, acc[db][4 * i4 + 3] * inv);
+        *reinterpret_cast<uint2 *>(dst + d) = make_uint2(w0, w1);
       }
+  } else {
+    const int64_t pr = (static_cast<int64_t>(slot) * num_kv_heads + kvh) * kRows + r;
+    float *dst = ws_acc + pr * kHeadDim;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int d = 32 * db + 8 * i4 + 4 * h;
+        *reinterpret_cast<f32x4 *>(dst + d) =
+            f32x4{acc[db][4 * i4], acc[db][4 * i4 + 1], acc[db][4 * i4 + 2],
+                  acc[db][4 * i4 + 3]};
+      }
+    if (h == 0) {
+      ws_ml[pr * 2 + 0] = m_run == -INFINITY ? -INFINITY : m_run * scale_log2;
+      ws_ml[pr * 2 + 1] = lsum;
     }
   }
 }
@@ -364,7 +383,8 @@ void launch_prefill(hipStream_t st, int num_kv_heads, int n_items, const uint16_
                     int64_t pool_hs, const int32_t *page_table, int64_t pt_stride,
                     const int32_t *q_start, const int32_t *kv_lens, const int32_t *items,
                     float *ws_acc, float *ws_ml, int page_shift, float scale_log2) {
-  hipLaunchKernelGGL(prefill_kernel<G>, dim3(num_kv_heads, n_items), dim3(256), 0, st, q, q_ss,
+  hipLaunchKernelGGL((prefill_kernel<G, kTileKeys>), dim3(num_kv_heads, n_items), dim3(kThreads), 0,
+                     st, q, q_ss,
                      q_st, q_sh, out, o_ss, o_st, o_sh, k_pool, v_pool, pool_hs, page_table,
                      pt_stride, q_start, kv_lens, items, ws_acc, ws_ml, num_kv_heads, page_shift,
                      scale_log2);
