@@ -6,7 +6,8 @@
 // whatever the spread of context lengths; a sequence with more than one
 // split gets consecutive workspace slots and one merge item for the merge
 // pass. Ranges are listed longest first.
-// Prefill sequences (q_len > 1) are cut into query tiles of 256 / G tokens;
+// Prefill sequences (q_len > 1) are cut into query tiles of kPrefillRows / G
+// tokens (prefill_shape.h);
 // the longest tiles are split along their key range when the simulated
 // dispatch says so, and work is ordered longest first so the short items
 // fill in behind the long ones.
@@ -21,6 +22,7 @@
 #include <vector>
 
 #include "../../include/hayate_attn.h"
+#include "prefill_shape.h"
 
 namespace hy {
 void set_error(const char *fmt, ...);
@@ -30,11 +32,15 @@ void clear_error();
 namespace {
 
 constexpr int kSlice = 32;        // decode kernel's token slice
-constexpr int kPrefillRows = 256;  // (token, head) rows of a prefill workgroup
-constexpr int kPrefillKeys = 64;   // keys per prefill step
-// Merge traffic of one prefill split partial (write + read of 256 rows of
-// fp32 O), in units of one prefill step of one workgroup.
-constexpr double kPartialCost = 0.05;
+using hy::kPrefillRows;                          // rows of a prefill workgroup
+constexpr int kPrefillKeys = hy::kPrefillTileKeys;  // keys per prefill step
+// Prefill cost model, in units of one step (64 keys) of one workgroup,
+// measured on MI355X: a workgroup's fixed cost (Q load, first tile,
+// epilogue) is about two steps; the merge launch about two steps; one
+// split partial (write + read of its rows of fp32 O) a fortieth of a step.
+constexpr double kPrefillFixed = 2.0;
+constexpr double kMergeLaunch = 2.0;
+constexpr double kPartialCost = 0.025;
 constexpr int kDecodeWgPerCu = 2;    // decode kernel occupancy (registers)
 constexpr int64_t kWgOverhead = 96;  // fixed cost of a workgroup, in tokens
 
@@ -72,30 +78,32 @@ int64_t decode_makespan(const std::vector<int64_t> &kvs, int64_t split, int num_
 }
 
 // Makespan (in steps) of prefill tiles cut into key ranges of at most
-// `max_steps` steps, dispatched longest first onto `slots` CUs, plus the
-// merge traffic of the partials they create.
+// `max_steps` steps, dispatched longest first onto `slots` workgroup slots
+// (each kv head a separate workgroup), plus the merge launch and the merge
+// traffic of the partials they create.
 double prefill_cost(const std::vector<int64_t> &tile_steps, int64_t max_steps, int num_kv_heads,
                     int64_t slots) {
-  std::vector<int64_t> costs;
+  std::vector<double> costs;
   int64_t partials = 0;
   for (int64_t st : tile_steps) {
     const int64_t n = (st + max_steps - 1) / max_steps;
     const int64_t per = (st + n - 1) / n;
-    for (int64_t a = 0; a < st; a += per) costs.push_back(std::min(per, st - a) + 1);
+    for (int64_t a = 0; a < st; a += per)
+      costs.push_back(static_cast<double>(std::min(per, st - a)) + kPrefillFixed);
     if (n > 1) partials += n;
   }
-  std::sort(costs.begin(), costs.end(), std::greater<int64_t>());
-  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> free_at;
-  for (int64_t i = 0; i < slots; ++i) free_at.push(0);
-  int64_t makespan = 0;
-  for (int64_t c : costs)
+  std::sort(costs.begin(), costs.end(), std::greater<double>());
+  std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
+  for (int64_t i = 0; i < slots; ++i) free_at.push(0.0);
+  double makespan = 0.0;
+  for (double c : costs)
     for (int h = 0; h < num_kv_heads; ++h) {
-      const int64_t t = free_at.top() + c;
+      const double t = free_at.top() + c;
       free_at.pop();
       free_at.push(t);
       makespan = std::max(makespan, t);
     }
-  return static_cast<double>(makespan) + kPartialCost * partials * num_kv_heads;
+  return makespan + (partials ? kMergeLaunch : 0.0) + kPartialCost * partials * num_kv_heads;
 }
 
 }  // namespace
@@ -215,7 +223,7 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
     it[3] = splits[i].slot;
   }
 
-  // Prefill: query tiles of 256 / G tokens; the key range of a tile is
+  // Prefill: query tiles of kPrefillRows / G tokens; the key range of a tile is
   // [0, cache_len + q_end). The longest tiles are split into key ranges of
   // at most max_steps 64-key steps when that shortens the simulated run.
   struct Tile {
@@ -240,10 +248,12 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
   if (!tiles.empty()) {
     std::vector<int64_t> tile_steps;
     for (const Tile &t : tiles) tile_steps.push_back(t.steps);
-    const int64_t slots = num_cus > 0 ? num_cus : 256;
+    const int64_t slots = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * hy::kPrefillWgPerCu;
     double best = prefill_cost(tile_steps, max_steps, num_kv_heads, slots);
-    const int64_t step = std::max<int64_t>(1, (max_steps - 4) / 16);
-    for (int64_t cand = max_steps - step; cand >= 4; cand -= step) {
+    // Candidates: every length down to 2 steps for short ranges, at most 32
+    // evenly spaced ones for long ranges (the simulation is cheap).
+    const int64_t step = std::max<int64_t>(1, (max_steps - 2) / 32);
+    for (int64_t cand = max_steps - step; cand >= 2; cand -= step) {
       const double t = prefill_cost(tile_steps, cand, num_kv_heads, slots);
       if (t < best) {
         best = t;

@@ -4,9 +4,11 @@
 // items in the planner's longest-first order and, with 8 kv heads on the 8
 // XCDs, every workgroup of one kv head lands on the same XCD (its L2 holds
 // that head's K/V pages for all query tiles of the request). An item is a
-// tile of 256 / G query tokens of one sequence; with its G query heads that
-// is 256 (token, head) rows, all reading the same K/V rows (GQA), over the
-// key range [kv_begin, kv_end) of one split.
+// tile of kPrefillRows / G query tokens of one sequence; with its G query
+// heads that is kPrefillRows (token, head) rows (prefill_shape.h), all
+// reading the same K/V rows (GQA), over the key range [kv_begin, kv_end) of
+// one split. Two 128-row workgroups share a CU, so one's prologue and
+// epilogue overlap the other's main loop.
 //
 // Eight waves of 32 rows, two waves per SIMD: while one wave of a SIMD runs
 // its softmax on the VALU the other one keeps the matrix core busy (a wave
@@ -49,17 +51,18 @@
 #include <type_traits>
 
 #include "hy_common.h"
+#include "prefill_shape.h"
 
 namespace hy {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kRows = 256;     // (token, head) rows per workgroup
-constexpr int kThreads = 512;  // eight waves of 32 rows
+constexpr int kRows = kPrefillRows;  // (token, head) rows per workgroup
+constexpr int kThreads = 2 * kRows;  // one wave per 32 rows
 constexpr int kKRow = 136;     // u16 per K row in LDS (272 bytes)
 constexpr int kVRow = 144;     // u16 per V row in LDS (288 bytes)
 constexpr float kLazy = 8.0f;  // rescale threshold, exp2 domain
-constexpr int kTileKeys = 64;  // keys per LDS stage: two 32-key blocks
+constexpr int kTileKeys = kPrefillTileKeys;  // keys per LDS stage
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -91,7 +94,9 @@ __device__ __forceinline__ float halves_sum(float x) {
 }
 
 template <int G, int KEYS>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(kPrefillWgPerCu * kThreads / 256, kPrefillWgPerCu * kThreads / 256)))
+void prefill_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
     uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
@@ -100,7 +105,9 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
     const int32_t *__restrict__ items, float *__restrict__ ws_acc, float *__restrict__ ws_ml,
     int num_kv_heads, int page_shift, float scale_log2) {
   static_assert(KEYS % 32 == 0 && KEYS >= 32, "tiles are whole 32-key blocks");
-  constexpr int kChunks = KEYS / 32;  // 16-byte K (and V) chunks per thread per tile
+  constexpr int kChunks = KEYS * 16 / kThreads;  // 16-byte K (and V) chunks per thread
+  constexpr int kPass = kThreads / 16;            // tile rows one chunk index covers
+  static_assert(KEYS * 16 % kThreads == 0 && kPass % 16 == 0, "staging covers whole rows");
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][KEYS * kKRow];
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][KEYS * kVRow];
 
@@ -137,6 +144,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
       u32x4 w = {0u, 0u, 0u, 0u};
       if (live) w = load16(src + 16 * kk + 8 * h);
       qop[kk] = __builtin_bit_cast(bf16x8, w);
+      // Scores come out of the MFMA in exp2 units: q * scale * log2(e),
+      // rounded to bf16 once here.
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        qop[kk][e] = static_cast<__bf16>(static_cast<float>(qop[kk][e]) * scale_log2);
     }
   }
 
@@ -145,8 +157,20 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
-  float m_run = -INFINITY;
+  // Exponent base of this lane's row, in exp2 units and bf16-exact; -inf
+  // until the row has seen a key. The QK^T chain subtracts it (as r_mma,
+  // 0 while unset) with one more MFMA: A = 1 in k index 0 (a constant), B =
+  // -r_mma in k index 0 of this row, so the scores come out shifted and the
+  // probabilities are plain exp2 of them.
+  float base = -INFINITY;
+  float r_mma = 0.f;
   float l_run = 0.f;
+  bf16x8 shift_a, shift_b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    shift_a[e] = static_cast<__bf16>(e == 0 && h == 0 ? 1.0f : 0.0f);
+    shift_b[e] = static_cast<__bf16>(0.0f);
+  }
 
   // Causal limits: this row sees keys <= limit; every live row of the wave
   // sees keys <= wave_lo; no live row of the wave sees a key > wave_hi.
@@ -164,20 +188,30 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
   const int page_mask = (1 << page_shift) - 1;
 
   // Staging: thread t moves chunk j < kChunks of the K and of the V tile:
-  // row 32 j + t / 16, dims 8 (t % 16) .. +7. Row group j (32 rows) lies in
-  // one page: one wave-uniform page lookup per group. Rows at or past kv_end
+  // row kPass j + t / 16, dims 8 (t % 16) .. +7. A 32-row group lies in one
+  // page: one wave-uniform page lookup per chunk. Rows at or past kv_end
   // read the last valid key instead (any finite data: their scores are
   // masked), so the loads need no branch.
   const int srow = tid >> 4;
   const int scol = (tid & 15) * 8;
-  auto load_tile = [&](int kt, u32x4(&kr)[kChunks], u32x4(&vr)[kChunks])
+  // Page ids of a tile's chunks (scalar loads), fetched one tile before the
+  // tile's loads so that no wave waits for them.
+  struct Pages {
+    int32_t id[kChunks];
+  };
+  auto fetch_pages = [&](int kt) __attribute__((always_inline)) {
+    Pages pg;
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j)
+      pg.id[j] = pt[min(kt + ((kPass * j) & ~31), last_key) >> page_shift];
+    return pg;
+  };
+  auto load_tile = [&](int kt, const Pages &pg, u32x4(&kr)[kChunks], u32x4(&vr)[kChunks])
                        __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
-      const int g0 = min(kt + 32 * j, last_key);
-      const int64_t page = pt[g0 >> page_shift];
-      const int key = min(kt + 32 * j + srow, last_key);
-      const int64_t p = (page << page_shift) + (key & page_mask);
+      const int key = min(kt + kPass * j + srow, last_key);
+      const int64_t p = (static_cast<int64_t>(pg.id[j]) << page_shift) + (key & page_mask);
       kr[j] = load16(kh + p * kHeadDim + scol);
       vr[j] = load16(vh + p * kHeadDim + scol);
     }
@@ -186,8 +220,8 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
                         __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
-      *reinterpret_cast<u32x4 *>(&sK[b][(32 * j + srow) * kKRow + scol]) = kr[j];
-      *reinterpret_cast<u32x4 *>(&sV[b][(32 * j + srow) * kVRow + scol]) = vr[j];
+      *reinterpret_cast<u32x4 *>(&sK[b][(kPass * j + srow) * kKRow + scol]) = kr[j];
+      *reinterpret_cast<u32x4 *>(&sV[b][(kPass * j + srow) * kVRow + scol]) = vr[j];
     }
   };
 
@@ -197,7 +231,6 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
   const int q16 = lane >> 4;
   const int k_base = c * kKRow + 8 * h;
   const int v_base = (4 * (q16 >> 1) + (r16 >> 2)) * kVRow + 16 * (q16 & 1) + 4 * (r16 & 3);
-  const float lazy_raw = kLazy / scale_log2;  // kLazy in raw score units
 
   // One 32-key block starting at key kb0, K/V rows at Kb/Vb in LDS.
   auto block = [&](auto masked, const uint16_t *Kb, const uint16_t *Vb, int kb0)
@@ -211,6 +244,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
       const bf16x8 kop = *reinterpret_cast<const bf16x8 *>(Kb + k_base + 16 * kk);
       s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[kk], s, 0, 0, 0);
     }
+    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s, 0, 0, 0);
     if constexpr (kMasked) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -218,27 +252,33 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
         if (key > limit) s[i] = -INFINITY;
       }
     }
-    float m = fmaxf(s[0], s[1]);
+    float mx = fmaxf(s[0], s[1]);
 #pragma unroll
-    for (int i = 2; i < 16; ++i) m = fmaxf(m, s[i]);
-    m = halves_max(m);
-    // m_run is the exponent base; it only moves when the row max exceeds it
-    // by more than kLazy in the exp2 domain (from -inf: at the first
-    // visible key), so probabilities stay below 2^kLazy.
-    if (__builtin_expect(__any(m > m_run + lazy_raw), 0)) {
-      const float m_new = fmaxf(m_run, m);
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-      m_run = m_new;
+    for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    mx = halves_max(mx);  // row max relative to r_mma
+    // The base only moves when the row max exceeds it by more than kLazy
+    // (from -inf: at the first visible key), so probabilities stay below
+    // 2^kLazy; the new base is the row max rounded to bf16.
+    const bool need = base == -INFINITY ? mx != -INFINITY : mx > kLazy;
+    if (__builtin_expect(__any(need), 0)) {
+      const float r_new = need ? __uint_as_float(f32_to_bf16_rne(mx + r_mma) << 16) : r_mma;
+      const float delta = r_new - r_mma;
+      const float alpha = base == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(-delta);
+      if (need) {
+        base = r_new;
+        r_mma = r_new;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] -= delta;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+      shift_b[0] = static_cast<__bf16>(h == 0 ? -r_mma : 0.0f);
     }
-    // A row whose keys are all masked so far keeps m = -inf: base 0 gives zeros.
-    const float mc = m_run == -INFINITY ? 0.f : m_run * scale_log2;
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], scale_log2, -mc));
+      const float p = __builtin_amdgcn_exp2f(s[i]);
       s[i] = p;
       psum += p;
     }
@@ -258,17 +298,19 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
       }
   };
 
+  const int n_tiles = (kv_end - kv_begin + KEYS - 1) / KEYS;
   {
     u32x4 kr[kChunks], vr[kChunks];
-    load_tile(kv_begin, kr, vr);
+    load_tile(kv_begin, fetch_pages(kv_begin), kr, vr);
     store_tile(0, kr, vr);
   }
+  Pages pg_next = {};
+  if (n_tiles > 1) pg_next = fetch_pages(kv_begin + KEYS);
   __syncthreads();
 
   // Tiles whose keys every live row of the workgroup sees need no mask
   // (they come first); the rest decide per wave and 32-key block whether to
   // skip, compute plainly or mask.
-  const int n_tiles = (kv_end - kv_begin + KEYS - 1) / KEYS;
   int n_plain = (min(cache_len + q_begin, last_key) + 1 - kv_begin) / KEYS;
   n_plain = n_plain < 0 ? 0 : (n_plain > n_tiles ? n_tiles : n_plain);
   auto iterate = [&](auto diag, int t) __attribute__((always_inline)) {
@@ -277,7 +319,10 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
     const int b = t & 1;
     const bool has_next = t + 1 < n_tiles;
     u32x4 kr[kChunks], vr[kChunks];
-    if (has_next) load_tile(kt + KEYS, kr, vr);
+    if (has_next) {
+      load_tile(kt + KEYS, pg_next, kr, vr);
+      if (t + 2 < n_tiles) pg_next = fetch_pages(kt + 2 * KEYS);
+    }
     if (wave_live) {
 #pragma unroll
       for (int kb = 0; kb < KEYS / 32; ++kb) {
@@ -334,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
                   acc[db][4 * i4 + 3]};
       }
     if (h == 0) {
-      ws_ml[pr * 2 + 0] = m_run == -INFINITY ? -INFINITY : m_run * scale_log2;
+      ws_ml[pr * 2 + 0] = base;
       ws_ml[pr * 2 + 1] = lsum;
     }
   }
@@ -405,6 +450,8 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 }  // namespace hy
 
 using hy::kHeadDim;
+
+extern "C" int32_t hy_prefill_tile_rows(void) { return hy::kRows; }
 
 extern "C" int64_t hy_prefill_workspace_bytes(int32_t n_slots, int32_t num_kv_heads,
                                               int32_t head_dim) {

@@ -69,6 +69,7 @@ _SIGNATURES = {
         [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P, _I64, _I32, _I32, _P],
         ctypes.c_int,
     ),
+    "hy_prefill_tile_rows": ([], ctypes.c_int32),
     "hy_prefill_workspace_bytes": ([_I32, _I32, _I32], ctypes.c_int64),
     "hy_paged_prefill": (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64,
@@ -156,14 +157,15 @@ def plan_tick(
     kv_lens = np.ascontiguousarray(kv_lens, dtype=np.int32)
     n = int(q_lens.shape[0])
     group = max(1, num_q_heads // max(1, num_kv_heads))
-    tile = max(1, 256 // group)
+    tile = max(1, int(lib().hy_prefill_tile_rows()) // group)
     split_floor = 32 if tokens_per_split <= 0 else max(32, tokens_per_split)
     dec_mask = q_lens == 1
     pre_mask = q_lens > 1
     dec_cap = int((kv_lens[dec_mask].astype(np.int64) // split_floor + 1).sum()) + 1
     n_tiles = int(((q_lens[pre_mask].astype(np.int64) + tile - 1) // tile).sum())
     max_steps = int((kv_lens.max() + 63) // 64) if n else 1
-    pre_cap = n_tiles * max(1, max_steps // 4 + 1) + 1
+    # the planner splits a tile into ranges of at least two 64-key steps
+    pre_cap = n_tiles * max(1, max_steps // 2 + 1) + 1
     dec = np.zeros((dec_cap, 4), dtype=np.int32)
     mrg = np.zeros((n + 1, 4), dtype=np.int32)
     pre = np.zeros((pre_cap, 8), dtype=np.int32)

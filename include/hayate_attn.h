@@ -190,8 +190,16 @@ int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,
                           int64_t workspace_bytes, int32_t num_q_heads,
                           int32_t head_dim, void *stream);
 
+/* (token, head) rows of one prefill query tile: hy_plan_tick cuts prefill
+ * sequences into tiles of hy_prefill_tile_rows() / G tokens (G = query heads
+ * per kv head), so callers size the prefill item list from it. Part of the
+ * work-list format that replaces the reference's BlockMask blocks
+ * (hayate/engine/paged_cache.py:273-284); no reference counterpart. */
+int32_t hy_prefill_tile_rows(void);
+
 /* Prefill split workspace bytes for n_slots partials (fp32 acc[head_dim],
- * max, sum for each of the 256 rows of a query tile, per kv head). */
+ * max, sum for each of the hy_prefill_tile_rows() rows of a query tile, per
+ * kv head). */
 int64_t hy_prefill_workspace_bytes(int32_t n_slots, int32_t num_kv_heads,
                                    int32_t head_dim);
 

@@ -76,7 +76,7 @@ def test_plan_prefill_tiles_cover_every_query_and_key_once():
     p = plan(q, kv)
     dec, pre = p.decode, p.prefill
     assert len(dec) >= 1 and (dec[:, 0] == 2).all()
-    tile = 256 // 4
+    tile = _native.lib().hy_prefill_tile_rows() // 4
     lengths = pre[:, 4] - pre[:, 3]
     assert (lengths[:-1] >= lengths[1:]).all()  # longest first
     assert (pre[:, 3] % 64 == 0).all()
