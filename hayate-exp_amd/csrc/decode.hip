@@ -63,7 +63,8 @@ struct SliceRegs {
 
 // Issues the 16 loads of the slice starting at logical token t0 (a multiple
 // of 32, so the slice lies in one page) into registers. t0 and the page id
-// are wave-uniform, so the page-table read is a scalar load.
+// are wave-uniform, so the page-table read is a scalar load. Every K/V row
+// is read once per launch: the loads are nontemporal.
 __device__ __forceinline__ void issue_slice(SliceRegs &r, const uint16_t *__restrict__ kh,
                                             const uint16_t *__restrict__ vh,
                                             const int32_t *__restrict__ pt, int t0,
@@ -76,12 +77,12 @@ __device__ __forceinline__ void issue_slice(SliceRegs &r, const uint16_t *__rest
   const int g = lane >> 4;
   // V first: it is consumed (staged into LDS) before the K registers.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r.v[i] = load16(vb + (4 * i + g) * kHeadDim + n * 8);
+  for (int i = 0; i < 8; ++i) r.v[i] = load16_stream(vb + (4 * i + g) * kHeadDim + n * 8);
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      r.k[b][kk] = load16(kb + (16 * b + n) * kHeadDim + kk * 32 + g * 8);
+      r.k[b][kk] = load16_stream(kb + (16 * b + n) * kHeadDim + kk * 32 + g * 8);
   // Keep the issue group together so that a consumer placed after it waits
   // only for the loads issued before the group.
   __builtin_amdgcn_sched_barrier(0);

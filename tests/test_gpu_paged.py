@@ -248,3 +248,40 @@ def test_gather_scatter_round_trip_bit_exact():
     # against the oracle's gather over the same pool
     pool = bits(m.k_cache[:, 0])
     assert np.array_equal(bits(snap.k), R.page_gather(pool, h.pages, 650, 128))
+
+
+def test_graph_replay_matches_eager():
+    """One mixed tick (append + decode + prefill + merges) captured in a HIP
+    graph: every replay, with eager work and synchronisations between
+    replays, reproduces the eager step bit for bit."""
+    say("[graph replay mixed_tick]")
+    w = make_workload("mixed_tick", device=DEV, num_layers=1)
+    batch = w.begin()
+    batch.plan(w.q.shape[1])
+
+    def step():
+        q_rot = batch.norm_rope_write_layer(0, w.q, w.k, w.v, w.q_norm_w, w.k_norm_w, EPS,
+                                            w.cos, w.sin)
+        return q_rot, batch.attend_layer(q_rot, 0)
+
+    q_eager, out_eager = step()
+    torch.cuda.synchronize()
+    q_eager, out_eager = bits(q_eager), bits(out_eager)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        q_g, out_g = step()
+    scratch = torch.randn(1 << 20, device=DEV)
+    for rep in range(3):
+        q_g.zero_()
+        out_g.zero_()
+        scratch.mul_(1.5).sum().item()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(q_g), q_eager), f"replay {rep}: rotated q differs"
+        assert np.array_equal(bits(out_g), out_eager), f"replay {rep}: attention differs"
