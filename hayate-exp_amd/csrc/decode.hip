@@ -1,21 +1,33 @@
-// Split-K GQA paged decode attention (one query token per sequence).
+// Stream-K GQA paged decode attention (one query token per sequence).
 //
-// Grid: (kv head, decode item). A workgroup of 4 waves owns one token range
-// [tok_begin, tok_end) of one sequence (a "split") and one kv head, and
-// serves all G = num_q_heads / num_kv_heads query heads of that kv head from
-// a single read of every K/V row (GQA sharing).
+// Work split: the K/V rows of all decode sequences, in sequence order, form
+// one token stream per kv head; the planner cuts it into chunks of equal
+// length, one per CU and kv head, so every workgroup streams the same number
+// of bytes whatever the spread of context lengths. A chunk holds one or more
+// pieces (the part of one sequence inside the chunk). Grid: (kv head,
+// chunk); with 8 kv heads, XCD i streams head i. A workgroup serves all
+// G = num_q_heads / num_kv_heads query heads of its kv head from a single
+// read of every K/V row (GQA sharing).
 //
-// The range is walked in 32-token slices (a slice never crosses a page since
-// page_size is a power of two >= 32); wave w takes slices w, w + 4, ... and
-// keeps its own online-softmax state, so waves never synchronise until the
-// end. Both products run on v_mfma_f32_16x16x32_bf16 (lane l, n = l % 16,
+// The chunk is walked in 32-token slices (a slice never crosses a page since
+// page_size is a power of two >= 32 and cuts fall on multiples of 32); wave
+// w of W takes slices w, w + W, ... and keeps its own online-softmax state
+// for the piece it is in, so waves never synchronise after the start. When
+// a wave moves to a new piece it writes its partial (acc, max, sum) of the
+// old one to the workspace, and decode_merge_kernel (a second launch on the
+// same stream: the kernel boundary publishes the partials) combines the W
+// partials of every piece of a sequence. One workgroup per CU with two waves
+// keeps HBM busiest; more waves per CU only add contention.
+//
+// Both products run on v_mfma_f32_16x16x32_bf16 (lane l, n = l % 16,
 // g = l / 16):
 //
 //   S = K Q^T   A = K rows (16 tokens x 32 dims), loaded from HBM straight
 //               into registers (lane n reads 16 B of row n, a whole 256-byte
-//               row per 16 lanes); B = Q^T, column n < G is query head n.
-//               Lane (n, g) ends with the scores of head n for the slice
-//               tokens 4g + i and 16 + 4g + i (i < 4).
+//               row per 16 lanes); B = Q^T, column n < G is query head n,
+//               read from an LDS table of the chunk's query rows built at
+//               the start. Lane (n, g) ends with the scores of head n for
+//               the slice tokens 4g + i and 16 + 4g + i (i < 4).
 //   O^T += V^T P^T  B = P^T must give lane (n, g) eight probabilities of
 //               head n: exactly its own eight scores, once MFMA k index
 //               8g + j stands for token (j < 4 ? 4g + j : 16 + 4g + j - 4).
@@ -28,25 +40,19 @@
 //               any LDS read, which serialises the prefetch below.)
 //
 // V rows sit in LDS with a 288-byte stride so that the four rows one
-// transposed read touches start 8 banks apart. The K and V registers are double
-// buffered: slice s + 4 is in flight while slice s is consumed. Rows past the
-// end of the context may hold any bits; their scores are masked and their V
-// values zeroed before the MFMA so that 0 * NaN never occurs.
-//
-// The end of a split merges the four waves in LDS and writes either the bf16
-// output (single split) or an fp32 partial (acc, max, sum) to the workspace;
-// decode_merge_kernel then combines the partials of each split sequence
-// (log-sum-exp). The merge is a second launch (hy_paged_decode_merge) on the
-// same stream: the kernel boundary publishes the partials without any
-// device-scope fence.
+// transposed read touches start 8 banks apart. The K and V registers are
+// double buffered: slice k + W is in flight while slice k is consumed. Rows
+// past the end of a context may hold any bits; their scores are masked and
+// their V values zeroed before the MFMA so that 0 * NaN never occurs.
 
+#include "decode_shape.h"
 #include "hy_common.h"
 
 namespace hy {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kWaves = 4;
+constexpr int kWaves = kDecodeWaves;
 constexpr int kSlice = 32;                       // tokens per slice
 constexpr int kVRow = kHeadDim + 16;             // LDS V row stride (u16): 288 bytes
 constexpr int kSliceElems = kSlice * kVRow;      // u16 per V transpose buffer
@@ -195,32 +201,54 @@ __device__ __forceinline__ void consume_slice(const SliceRegs &r, const uint16_t
   }
 }
 
-// Two waves per SIMD (two workgroups per CU): the double-buffered slice
-// registers need about 240 VGPRs.
+// Token range of one piece (part of one sequence inside one chunk), as
+// read from its record {seq, tok_begin, tok_end, slot_base, slice_begin,
+// q_tok, 0, 0}.
+struct Piece {
+  int seq, t0, t1, slot, sb, qt, nsl;
+};
+
+__device__ __forceinline__ Piece load_piece(const int32_t *pieces, int p) {
+  const int32_t *r = pieces + 8 * p;
+  Piece x;
+  x.seq = r[0];
+  x.t0 = r[1];
+  x.t1 = r[2];
+  x.slot = r[3];
+  x.sb = r[4];
+  x.qt = r[5];
+  x.nsl = (x.t1 - x.t0 + kSlice - 1) / kSlice;
+  return x;
+}
+
+// Where an issued slice lies: its piece, first token and the piece's end.
+struct SliceMeta {
+  int piece, t0, tend;
+};
+
+// Two waves per SIMD: the double-buffered slice registers (K, V and the
+// query operand of each slice) need about 240 VGPRs.
 template <int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
-    uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
     int64_t pool_hs, const int32_t *__restrict__ page_table, int64_t pt_stride,
-    const int32_t *__restrict__ q_start, const int32_t *__restrict__ items,
-    float *__restrict__ ws_acc, float *__restrict__ ws_ml, int num_q_heads,
-    int page_shift, float scale_log2) {
-  // One V transpose buffer per wave; it also holds the cross-wave merge at
-  // the end when that fits.
+    const int32_t *__restrict__ items, int n_chunks, float *__restrict__ ws_acc,
+    float *__restrict__ ws_ml, int num_q_heads, int page_shift, float scale_log2) {
+  // One V transpose buffer per wave, and the query rows (G heads) of every
+  // piece of the chunk.
   __shared__ __attribute__((aligned(16))) uint16_t sV[kWaves][kSliceElems];
-  constexpr int kMergeFloats = kWaves * G * kHeadDim + 2 * kWaves * G;
-  constexpr bool kMergeInV = kMergeFloats * sizeof(float) <= sizeof(sV);
-  __shared__ float sMergeExtra[kMergeInV ? 1 : kMergeFloats];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[kDecodeQTableBytes / 2];
+  constexpr int kMaxPieces = kDecodeQTableBytes / (G * kHeadDim * 2);
 
-  // Grid (kv head, item): heads vary fastest so the dispatcher walks the
-  // items in the planner's longest-first order.
-  const int32_t *it = items + 4 * blockIdx.y;
+  // Grid (kv head, chunk): heads vary fastest, so with 8 kv heads every
+  // XCD streams one head.
+  const int32_t *ch = items + 8 * blockIdx.y;
+  const int32_t *pieces = items + 8 * n_chunks;
   const int kvh = blockIdx.x;
-  const int seq = it[0];
-  const int tok_begin = it[1];
-  const int tok_end = it[2];
-  const int slot = it[3];
+  const int pb = ch[0];
+  const int pe = ch[1];
+  const int n_sl = ch[2];
 
   // Wave index as a scalar: every per-slice address below is wave-uniform.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -228,112 +256,145 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int n = lane & 15;
   const int g = lane >> 4;
   const int h0 = kvh * G;
+  const uint16_t *kh = k_pool + kvh * pool_hs;
+  const uint16_t *vh = v_pool + kvh * pool_hs;
+  uint16_t *vbuf = sV[wave];
+  const uint16_t *vt_base = vbuf + (4 * g + (n >> 2)) * kVRow + 4 * (n & 3);
 
-  // Q^T operand: column n < G is query head h0 + n (the sequence's token).
-  const int64_t q_row = seq * q_ss + static_cast<int64_t>(q_start[seq]) * q_st;
-  bf16x8 qop[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    u32x4 w = {0u, 0u, 0u, 0u};
-    if (n < G) w = load16(q + q_row + (h0 + n) * q_sh + kk * 32 + g * 8);
-    qop[kk] = __builtin_bit_cast(bf16x8, w);
-  }
+  // Issue cursor: the piece holding the next slice to load (the chunk
+  // record repeats its first piece).
+  int ip = pb;
+  Piece ipc;
+  ipc.seq = ch[3];
+  ipc.t0 = ch[4];
+  ipc.t1 = ch[5];
+  ipc.slot = ch[6];
+  ipc.sb = 0;
+  ipc.qt = ch[7];
+  ipc.nsl = (ipc.t1 - ipc.t0 + kSlice - 1) / kSlice;
+  // Loads slice k of the chunk (k-th 32-token slice in piece order) into r.
+  auto issue = [&](SliceRegs &r, SliceMeta &m, int k) {
+    while (k >= ipc.sb + ipc.nsl) ipc = load_piece(pieces, ++ip);
+    const int t0 = ipc.t0 + (k - ipc.sb) * kSlice;
+    issue_slice(r, kh, vh, page_table + ipc.seq * pt_stride, t0, page_shift, lane);
+    m.piece = ip;
+    m.t0 = t0;
+    m.tend = ipc.t1;
+  };
 
+  // Online-softmax state of the piece being accumulated (cp).
+  int cp = pb;
+  int c_slot = ipc.slot;
   float m_run = -INFINITY;  // running max of head n (raw scores)
   float l_run = 0.f;        // lane-partial sum of head n
   f32x4 acc[8];             // O^T[16 db + 4g + i][head n]
 #pragma unroll
   for (int db = 0; db < 8; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const uint16_t *kh = k_pool + kvh * pool_hs;
-  const uint16_t *vh = v_pool + kvh * pool_hs;
-  const int32_t *pt = page_table + seq * pt_stride;
-  const int n_slices = (tok_end - tok_begin + kSlice - 1) / kSlice;
-  uint16_t *vbuf = sV[wave];
-  const uint16_t *vt_base = vbuf + (4 * g + (n >> 2)) * kVRow + 4 * (n & 3);
-
-  // Double-buffered slice loop: the loads of slice s + 4 are in flight
-  // while slice s is consumed. A slice's V rows go to LDS before the next
-  // slice is issued, so at most one slice's V registers are live with two
-  // slices' K registers. The steady state issues unconditionally so that
-  // every wait covers only earlier loads; the tail is peeled.
-  if (wave < n_slices) {
-    SliceRegs ra, rb;
-    int s = wave;
-    issue_slice(ra, kh, vh, pt, tok_begin + kSlice * s, page_shift, lane);
-    while (s + 2 * kWaves < n_slices) {
-      stage_v(ra, vbuf, lane);
-      issue_slice(rb, kh, vh, pt, tok_begin + kSlice * (s + kWaves), page_shift, lane);
-      consume_slice<G>(ra, vt_base, qop, tok_begin + kSlice * s, tok_end, lane, scale_log2,
-                       m_run, l_run, acc);
-      stage_v(rb, vbuf, lane);
-      issue_slice(ra, kh, vh, pt, tok_begin + kSlice * (s + 2 * kWaves), page_shift, lane);
-      consume_slice<G>(rb, vt_base, qop, tok_begin + kSlice * (s + kWaves), tok_end, lane,
-                       scale_log2, m_run, l_run, acc);
-      s += 2 * kWaves;
-    }
-    stage_v(ra, vbuf, lane);
-    if (s + kWaves < n_slices) {
-      issue_slice(rb, kh, vh, pt, tok_begin + kSlice * (s + kWaves), page_shift, lane);
-      consume_slice<G>(ra, vt_base, qop, tok_begin + kSlice * s, tok_end, lane, scale_log2,
-                       m_run, l_run, acc);
-      stage_v(rb, vbuf, lane);
-      consume_slice<G>(rb, vt_base, qop, tok_begin + kSlice * (s + kWaves), tok_end, lane,
-                       scale_log2, m_run, l_run, acc);
-    } else {
-      consume_slice<G>(ra, vt_base, qop, tok_begin + kSlice * s, tok_end, lane, scale_log2,
-                       m_run, l_run, acc);
-    }
-  }
-
-  // Wave totals of the row sums (the four 16-lane rows hold disjoint tokens).
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
-  __syncthreads();  // every wave is done with its V buffer
-  float *sm_acc = kMergeInV ? reinterpret_cast<float *>(&sV[0][0]) : sMergeExtra;
-  float *sm_m = sm_acc + kWaves * G * kHeadDim;             // [wave][G]
-  float *sm_l = sm_m + kWaves * G;                          // [wave][G]
-  if (n < G) {
+  // Writes this wave's partial (acc, max in the exp2 domain, sum) of the
+  // current piece to workspace slot `slot`; every wave owns one slot of
+  // every piece of its chunk.
+  auto flush = [&](int slot) {
+    float l = l_run;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (n < G) {
+      const int64_t base = static_cast<int64_t>(slot) * num_q_heads + h0 + n;
+      float *dst = ws_acc + base * kHeadDim + 4 * g;
 #pragma unroll
-    for (int db = 0; db < 8; ++db)
+      for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4 *>(dst + 16 * db) = acc[db];
+      if (g == 0) {
+        ws_ml[base * 2 + 0] = m_run * scale_log2;
+        ws_ml[base * 2 + 1] = l;
+      }
+    }
+  };
+  auto reset = [&]() {
+    m_run = -INFINITY;
+    l_run = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        sm_acc[(wave * G + n) * kHeadDim + 16 * db + 4 * g + i] = acc[db][i];
-    if (g == 0) {
-      sm_m[wave * G + n] = m_run;
-      sm_l[wave * G + n] = l_run;
+    for (int db = 0; db < 8; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  // Q^T operand of piece p: column n < G is query head h0 + n of its
+  // sequence's token.
+  bf16x8 qop[4];
+  auto load_q = [&](int p) {
+    const int j = p - pb;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (n < G && j < kMaxPieces)
+        w = *reinterpret_cast<const u32x4 *>(sQ + (j * G + n) * kHeadDim + kk * 32 + g * 8);
+      qop[kk] = __builtin_bit_cast(bf16x8, w);
+    }
+  };
+  // Closes the current piece and every piece before p that this wave has
+  // no slice of (their partials are empty), then starts piece p.
+  auto move_to = [&](int p) {
+    flush(c_slot + wave);
+    reset();
+    for (int x = cp + 1; x < p; ++x) flush(pieces[8 * x + 3] + wave);
+    cp = p;
+    c_slot = pieces[8 * p + 3];
+    load_q(p);
+  };
+
+  // The first slice's loads go out before the query table is built: all
+  // threads copy the query rows of the chunk's pieces into LDS, 16 bytes
+  // each (the planner keeps a chunk within kMaxPieces pieces).
+  int k = wave;
+  SliceRegs ra, rb;
+  SliceMeta ma, mb;
+  if (k < n_sl) issue(ra, ma, k);
+  {
+    const int n_p = min(pe - pb, kMaxPieces);
+    for (int idx = threadIdx.x; idx < n_p * G * 16; idx += kWaves * 64) {
+      const int j = idx / (G * 16);
+      const int h = (idx / 16) % G;
+      const int c = idx % 16;
+      const int32_t *pr = pieces + 8 * (pb + j);
+      const uint16_t *src = q + pr[0] * q_ss + static_cast<int64_t>(pr[5]) * q_st +
+                            (h0 + h) * q_sh + c * 8;
+      *reinterpret_cast<u32x4 *>(sQ + (j * G + h) * kHeadDim + c * 8) = load16(src);
     }
   }
   __syncthreads();
+  load_q(pb);
 
-  // Merge the four waves; thread t handles (head, dim) pairs.
-  const int64_t out_row = seq * o_ss + static_cast<int64_t>(q_start[seq]) * o_st;
-  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += 256) {
-    const int h = idx / kHeadDim;
-    const int d = idx % kHeadDim;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w * G + h]);
-    float lsum = 0.f, a = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw = sm_m[w * G + h];
-      const float f = mw == -INFINITY ? 0.f : exp2f((mw - mx) * scale_log2);
-      lsum += f * sm_l[w * G + h];
-      a += f * sm_acc[(w * G + h) * kHeadDim + d];
+  // Wave w takes slices w, w + 4, ... of the chunk. Double-buffered: the
+  // loads of slice k + 4 are in flight while slice k is consumed; a slice's
+  // V rows go to LDS before the next slice is issued. The steady state
+  // issues unconditionally so that every wait covers only earlier loads;
+  // the tail is peeled.
+  if (k < n_sl) {
+    while (k + 2 * kWaves < n_sl) {
+      stage_v(ra, vbuf, lane);
+      issue(rb, mb, k + kWaves);
+      if (ma.piece != cp) move_to(ma.piece);
+      consume_slice<G>(ra, vt_base, qop, ma.t0, ma.tend, lane, scale_log2, m_run, l_run, acc);
+      stage_v(rb, vbuf, lane);
+      issue(ra, ma, k + 2 * kWaves);
+      if (mb.piece != cp) move_to(mb.piece);
+      consume_slice<G>(rb, vt_base, qop, mb.t0, mb.tend, lane, scale_log2, m_run, l_run, acc);
+      k += 2 * kWaves;
     }
-    const int hq = h0 + h;
-    if (slot < 0) {
-      out[out_row + hq * o_sh + d] = static_cast<uint16_t>(f32_to_bf16_rne(a / lsum));
+    stage_v(ra, vbuf, lane);
+    if (k + kWaves < n_sl) {
+      issue(rb, mb, k + kWaves);
+      if (ma.piece != cp) move_to(ma.piece);
+      consume_slice<G>(ra, vt_base, qop, ma.t0, ma.tend, lane, scale_log2, m_run, l_run, acc);
+      stage_v(rb, vbuf, lane);
+      if (mb.piece != cp) move_to(mb.piece);
+      consume_slice<G>(rb, vt_base, qop, mb.t0, mb.tend, lane, scale_log2, m_run, l_run, acc);
     } else {
-      const int64_t base = static_cast<int64_t>(slot) * num_q_heads + hq;
-      ws_acc[base * kHeadDim + d] = a;
-      if (d == 0) {
-        ws_ml[base * 2 + 0] = mx * scale_log2;  // max in the exp2 domain
-        ws_ml[base * 2 + 1] = lsum;
-      }
+      if (ma.piece != cp) move_to(ma.piece);
+      consume_slice<G>(ra, vt_base, qop, ma.t0, ma.tend, lane, scale_log2, m_run, l_run, acc);
     }
   }
+  // Close the last piece and any later ones this wave had no slice of.
+  flush(c_slot + wave);
+  reset();
+  for (int x = cp + 1; x < pe; ++x) flush(pieces[8 * x + 3] + wave);
 }
 
 // Combines the partials of split sequences: grid (merge item, q head),
@@ -380,14 +441,13 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(
 
 template <int G>
 void launch_decode(hipStream_t st, dim3 grid, const uint16_t *q, int64_t q_ss, int64_t q_st,
-                   int64_t q_sh, uint16_t *out, int64_t o_ss, int64_t o_st, int64_t o_sh,
-                   const uint16_t *k_pool, const uint16_t *v_pool, int64_t pool_hs,
-                   const int32_t *page_table, int64_t pt_stride, const int32_t *q_start,
-                   const int32_t *items, float *ws_acc, float *ws_ml, int num_q_heads,
-                   int page_shift, float scale_log2) {
-  hipLaunchKernelGGL(decode_kernel<G>, grid, dim3(256), 0, st, q, q_ss, q_st, q_sh, out, o_ss,
-                     o_st, o_sh, k_pool, v_pool, pool_hs, page_table, pt_stride, q_start, items,
-                     ws_acc, ws_ml, num_q_heads, page_shift, scale_log2);
+                   int64_t q_sh, const uint16_t *k_pool, const uint16_t *v_pool, int64_t pool_hs,
+                   const int32_t *page_table, int64_t pt_stride, const int32_t *items,
+                   int n_chunks, float *ws_acc, float *ws_ml, int num_q_heads, int page_shift,
+                   float scale_log2) {
+  hipLaunchKernelGGL(decode_kernel<G>, grid, dim3(kWaves * 64), 0, st, q, q_ss, q_st, q_sh, k_pool,
+                     v_pool, pool_hs, page_table, pt_stride, items, n_chunks, ws_acc, ws_ml,
+                     num_q_heads, page_shift, scale_log2);
 }
 
 // Workspace layout: [acc fp32 n_slots*Hq*D][max,sum fp32 n_slots*Hq*2],
@@ -430,34 +490,32 @@ extern "C" int hy_paged_decode(
   if (n_decode == 0) return HY_OK;
   HY_REQUIRE(q && out && k_pool && v_pool && page_table && q_start && decode_items,
              "hy_paged_decode: null pointer argument");
+  const int G = num_q_heads / num_kv_heads;
+  HY_REQUIRE_SUPPORTED(G == 1 || G == 2 || G == 4 || G == 8 || G == 16,
+                       "GQA group size %d unsupported (1, 2, 4, 8, 16)", G);
+  HY_REQUIRE(n_slots > 0, "decode work needs workspace slots");
   const int64_t need = hy_decode_workspace_bytes(n_slots, num_q_heads, head_dim);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+  if (workspace == nullptr || workspace_bytes < need) {
     hy::set_error("workspace too small: need %lld bytes, got %lld",
                   static_cast<long long>(need), static_cast<long long>(workspace_bytes));
     return HY_ENOSPACE;
   }
-  float *ws_acc = nullptr, *ws_ml = nullptr;
-  if (need > 0) {
-    ws_acc = static_cast<float *>(workspace);
-    ws_ml = reinterpret_cast<float *>(
-        static_cast<char *>(workspace) +
-        hy::align256(static_cast<int64_t>(n_slots) * num_q_heads * head_dim * 4));
-  }
-  const int G = num_q_heads / num_kv_heads;
+  float *ws_acc = static_cast<float *>(workspace);
+  float *ws_ml = reinterpret_cast<float *>(
+      static_cast<char *>(workspace) +
+      hy::align256(static_cast<int64_t>(n_slots) * num_q_heads * head_dim * 4));
   const float scale_log2 = scale * hy::kLog2e;
   const int page_shift = __builtin_ctz(static_cast<unsigned>(page_size));
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid(num_kv_heads, n_decode);
   const uint16_t *qq = static_cast<const uint16_t *>(q);
-  uint16_t *oo = static_cast<uint16_t *>(out);
   const uint16_t *kp = static_cast<const uint16_t *>(k_pool);
   const uint16_t *vp = static_cast<const uint16_t *>(v_pool);
 #define HY_DECODE_CASE(GG)                                                                    \
   case GG:                                                                                    \
-    hy::launch_decode<GG>(st, grid, qq, q_stride_seq, q_stride_tok, q_stride_head, oo,        \
-                          o_stride_seq, o_stride_tok, o_stride_head, kp, vp, pool_head_stride, \
-                          page_table, page_table_stride, q_start, decode_items, ws_acc, ws_ml, \
-                          num_q_heads, page_shift, scale_log2);                               \
+    hy::launch_decode<GG>(st, grid, qq, q_stride_seq, q_stride_tok, q_stride_head, kp, vp,    \
+                          pool_head_stride, page_table, page_table_stride, decode_items,      \
+                          n_decode, ws_acc, ws_ml, num_q_heads, page_shift, scale_log2);      \
     break;
   switch (G) {
     HY_DECODE_CASE(1)

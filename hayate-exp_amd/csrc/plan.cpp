@@ -1,11 +1,11 @@
 // Tick planner: turns per-sequence (q_len, kv_len) into the work lists the
 // decode and prefill kernels consume. Host-only code, no device access.
 //
-// Decode sequences (q_len == 1) are cut into token ranges ("splits") of equal
-// size so that every workgroup streams about the same number of K/V bytes,
-// whatever the spread of context lengths; a sequence with more than one
-// split gets consecutive workspace slots and one merge item for the merge
-// pass. Ranges are listed longest first.
+// Decode sequences (q_len == 1): their K/V rows, concatenated in sequence
+// order, are cut into one chunk per CU and kv head, equal in length (cuts
+// inside a sequence on multiples of 32 tokens); each piece of a sequence in
+// a chunk gets W workspace slots (one per wave of the decode workgroup) and
+// every decode sequence one merge item over its pieces' slots.
 // Prefill sequences (q_len > 1) are cut into query tiles of kPrefillRows / G
 // tokens (prefill_shape.h);
 // the longest tiles are split along their key range when the simulated
@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "../../include/hayate_attn.h"
+#include "decode_shape.h"
 #include "prefill_shape.h"
 
 namespace hy {
@@ -41,41 +42,9 @@ constexpr int kPrefillKeys = hy::kPrefillTileKeys;  // keys per prefill step
 constexpr double kPrefillFixed = 2.0;
 constexpr double kMergeLaunch = 2.0;
 constexpr double kPartialCost = 0.025;
-constexpr int kDecodeWgPerCu = 2;    // decode kernel occupancy (registers)
-constexpr int64_t kWgOverhead = 96;  // fixed cost of a workgroup, in tokens
-
-int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
-
-// Length of each split of a kv_len-token context cut at about `split`.
-int64_t split_len(int64_t kv, int64_t split) {
-  const int64_t nsplit = (kv + split - 1) / split;
-  return round_up((kv + nsplit - 1) / nsplit, kSlice);
-}
-
-// Makespan of the decode grid when splits of about `split` tokens are
-// dispatched longest first onto `slots` workgroup slots, each kv head a
-// separate workgroup (cost model: tokens + fixed overhead).
-int64_t decode_makespan(const std::vector<int64_t> &kvs, int64_t split, int num_kv_heads,
-                        int64_t slots) {
-  std::vector<int64_t> costs;
-  for (int64_t kv : kvs) {
-    const int64_t len = split_len(kv, split);
-    for (int64_t t = 0; t < kv; t += len)
-      costs.push_back(std::min(len, kv - t) + kWgOverhead);
-  }
-  std::sort(costs.begin(), costs.end(), std::greater<int64_t>());
-  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> free_at;
-  for (int64_t i = 0; i < slots; ++i) free_at.push(0);
-  int64_t makespan = 0;
-  for (int64_t c : costs)
-    for (int h = 0; h < num_kv_heads; ++h) {
-      const int64_t t = free_at.top() + c;
-      free_at.pop();
-      free_at.push(t);
-      makespan = std::max(makespan, t);
-    }
-  return makespan;
-}
+constexpr int kDecodeWgPerCu = 1;     // decode workgroups (chunks) per CU
+using hy::kDecodeWaves;                // waves per decode workgroup: partials per piece
+constexpr int64_t kMinChunk = 256;    // smallest decode chunk, in tokens
 
 // Makespan (in steps) of prefill tiles cut into key ranges of at most
 // `max_steps` steps, dispatched longest first onto `slots` workgroup slots
@@ -147,80 +116,118 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
     if (q_lens[b] == 1) decode_tokens += kv_lens[b];
   }
 
-  // Split length: the candidate (a multiple of 128 tokens, at least 256 so
-  // that each wave keeps two slices) whose longest-first dispatch onto the
-  // GPU's workgroup slots finishes first; ties go to fewer splits.
-  int64_t split = target_tokens_per_split;
-  if (split <= 0) {
-    std::vector<int64_t> kvs;
-    int64_t max_kv = 0;
-    for (int b = 0; b < num_seqs; ++b)
-      if (q_lens[b] == 1) {
-        kvs.push_back(kv_lens[b]);
-        max_kv = std::max<int64_t>(max_kv, kv_lens[b]);
-      }
-    const int64_t slots = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * kDecodeWgPerCu;
-    split = std::max<int64_t>(256, round_up(std::max<int64_t>(max_kv, 1), 128));
-    int64_t best = kvs.empty() ? 0 : decode_makespan(kvs, split, num_kv_heads, slots);
-    // At most 16 candidates between 256 and the longest context.
-    const int64_t step = std::max<int64_t>(128, round_up((split - 256) / 16, 128));
-    for (int64_t cand = split - step; cand >= 256 && !kvs.empty(); cand -= step) {
-      const int64_t t = decode_makespan(kvs, cand, num_kv_heads, slots);
-      if (t < best) {
-        best = t;
-        split = cand;
-      }
+  // Decode: the K/V rows of all decode sequences, concatenated in sequence
+  // order, form one token stream per kv head that is cut into n_chunks
+  // chunks of equal length, one workgroup each. A cut inside a sequence
+  // falls on a multiple of 32 tokens of that sequence. A chunk holds one or
+  // more pieces (the part of one sequence inside the chunk); each wave of a
+  // chunk's workgroup leaves one partial per piece, and the merge pass
+  // combines all partials of a sequence.
+  std::vector<int32_t> q_begin(static_cast<size_t>(num_seqs) + 1, 0);
+  for (int b = 0; b < num_seqs; ++b) q_begin[b + 1] = q_begin[b] + q_lens[b];
+  int64_t n_chunks = 0;
+  if (decode_tokens > 0) {
+    if (target_tokens_per_split > 0) {
+      n_chunks = (decode_tokens + target_tokens_per_split - 1) / target_tokens_per_split;
+    } else {
+      const int64_t cus = num_cus > 0 ? num_cus : 256;
+      n_chunks = std::max<int64_t>(1, (cus * kDecodeWgPerCu + num_kv_heads - 1) / num_kv_heads);
+      n_chunks = std::min<int64_t>(n_chunks, std::max<int64_t>(1, decode_tokens / kMinChunk));
     }
-  } else {
-    split = round_up(split, kSlice);
   }
-
-  struct Split {
-    int32_t seq, t0, t1, slot;
+  struct PieceRec {
+    int32_t seq, t0, t1, slice_begin;
   };
-  std::vector<Split> splits;
-  int32_t n_merge = 0, n_pre = 0, n_slots = 0;
-  for (int b = 0; b < num_seqs; ++b) {
-    if (q_lens[b] != 1) continue;
-    const int64_t kv = kv_lens[b];
-    // Equal-length splits (a multiple of 32 each) instead of a short tail.
-    const int64_t len = split_len(kv, split);
-    const int64_t nsplit = (kv + len - 1) / len;
-    const bool merged = nsplit > 1;
-    for (int64_t s = 0; s < nsplit; ++s)
-      splits.push_back({b, static_cast<int32_t>(s * len),
-                        static_cast<int32_t>(std::min<int64_t>(kv, (s + 1) * len)),
-                        merged ? n_slots + static_cast<int32_t>(s) : -1});
-    if (merged) {
+  struct ChunkRec {
+    int32_t piece_begin, piece_end, n_slices;
+  };
+  std::vector<PieceRec> pieces;
+  std::vector<ChunkRec> chunks;
+  const int32_t max_pieces = hy::decode_max_pieces(G);
+  int32_t n_merge = 0, n_pre = 0;
+  {
+    int64_t pos = 0;        // stream position of the next token
+    int64_t chunk = 0;      // index of the chunk being filled
+    int32_t first = 0;      // its first piece
+    int32_t slices = 0;     // its slices so far
+    auto close_chunk = [&]() {
+      if (static_cast<int32_t>(pieces.size()) > first)
+        chunks.push_back({first, static_cast<int32_t>(pieces.size()), slices});
+      first = static_cast<int32_t>(pieces.size());
+      slices = 0;
+      ++chunk;
+    };
+    for (int b = 0; b < num_seqs; ++b) {
+      if (q_lens[b] != 1) continue;
+      const int64_t kv = kv_lens[b];
+      const int64_t seq_pos = pos;  // stream position of token 0
+      const int32_t seq_first = static_cast<int32_t>(pieces.size());
+      int64_t t = 0;
+      while (t < kv) {
+        int64_t end = kv;
+        bool cut = false;
+        if (chunk < n_chunks - 1) {
+          const int64_t chunk_end = decode_tokens * (chunk + 1) / n_chunks;
+          if (chunk_end - seq_pos < kv) {
+            end = std::min<int64_t>(kv, std::max<int64_t>(t, (chunk_end - seq_pos + kSlice / 2) /
+                                                               kSlice * kSlice));
+            cut = true;
+          }
+        }
+        if (end > t) {
+          pieces.push_back({b, static_cast<int32_t>(t), static_cast<int32_t>(end), slices});
+          slices += static_cast<int32_t>((end - t + kSlice - 1) / kSlice);
+          pos += end - t;
+          t = end;
+        }
+        // A chunk also ends at the size of the kernel's query table.
+        if (cut || static_cast<int32_t>(pieces.size()) - first >= max_pieces) close_chunk();
+      }
       if (n_merge >= merge_capacity) {
         hy::set_error("hy_plan_tick: merge capacity %d too small", merge_capacity);
         return HY_ENOSPACE;
       }
       int32_t *mt = merge_items + 4 * n_merge++;
+      const int32_t np = static_cast<int32_t>(pieces.size()) - seq_first;
       mt[0] = b;
-      mt[1] = n_slots;
-      mt[2] = static_cast<int32_t>(nsplit);
+      mt[1] = kDecodeWaves * seq_first;
+      mt[2] = kDecodeWaves * np;
       mt[3] = 0;
-      n_slots += static_cast<int32_t>(nsplit);
     }
+    if (static_cast<int32_t>(pieces.size()) > first)
+      chunks.push_back({first, static_cast<int32_t>(pieces.size()), slices});
   }
-  if (static_cast<int64_t>(splits.size()) > decode_capacity) {
-    hy::set_error("hy_plan_tick: decode capacity %d too small (need %zu)", decode_capacity,
-                  splits.size());
+  const int32_t n_dec = static_cast<int32_t>(chunks.size());
+  const int32_t n_pieces = static_cast<int32_t>(pieces.size());
+  const int32_t n_slots = kDecodeWaves * n_pieces;
+  if (static_cast<int64_t>(n_dec) + n_pieces > decode_capacity) {
+    hy::set_error("hy_plan_tick: decode capacity %d too small (need %d)", decode_capacity,
+                  n_dec + n_pieces);
     return HY_ENOSPACE;
   }
-  // Longest ranges first: the workgroup dispatcher then fills in the short
-  // ones behind them.
-  std::stable_sort(splits.begin(), splits.end(), [](const Split &a, const Split &b) {
-    return a.t1 - a.t0 > b.t1 - b.t0;
-  });
-  const int32_t n_dec = static_cast<int32_t>(splits.size());
+  // Chunk records carry their first piece so that a workgroup can issue its
+  // first loads after one dependent read.
   for (int32_t i = 0; i < n_dec; ++i) {
-    int32_t *it = decode_items + 4 * i;
-    it[0] = splits[i].seq;
-    it[1] = splits[i].t0;
-    it[2] = splits[i].t1;
-    it[3] = splits[i].slot;
+    int32_t *it = decode_items + 8 * i;
+    const PieceRec &f = pieces[chunks[i].piece_begin];
+    it[0] = chunks[i].piece_begin;
+    it[1] = chunks[i].piece_end;
+    it[2] = chunks[i].n_slices;
+    it[3] = f.seq;
+    it[4] = f.t0;
+    it[5] = f.t1;
+    it[6] = kDecodeWaves * chunks[i].piece_begin;
+    it[7] = q_begin[f.seq];
+  }
+  for (int32_t i = 0; i < n_pieces; ++i) {
+    int32_t *it = decode_items + 8 * (n_dec + i);
+    it[0] = pieces[i].seq;
+    it[1] = pieces[i].t0;
+    it[2] = pieces[i].t1;
+    it[3] = kDecodeWaves * i;
+    it[4] = pieces[i].slice_begin;
+    it[5] = q_begin[pieces[i].seq];
+    it[6] = it[7] = 0;
   }
 
   // Prefill: query tiles of kPrefillRows / G tokens; the key range of a tile is
@@ -315,5 +322,6 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
   counts_out[3] = n_pre;
   counts_out[4] = n_pmerge;
   counts_out[5] = n_pslots;
+  counts_out[6] = n_pieces;
   return HY_OK;
 }

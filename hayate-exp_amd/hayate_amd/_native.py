@@ -132,11 +132,17 @@ def check(rc: int, what: str) -> None:
 class TickPlan:
     """Host copy of one tick's work lists (hy_plan_tick)."""
 
-    __slots__ = ("decode", "merge", "n_slots", "prefill", "prefill_merge", "n_prefill_slots")
+    __slots__ = ("decode", "n_chunks", "merge", "n_slots", "prefill", "prefill_merge",
+                 "n_prefill_slots")
 
-    def __init__(self, decode, merge, n_slots, prefill, prefill_merge, n_prefill_slots):
-        self.decode = decode                # int32 (n, 4) {seq, tok_begin, tok_end, slot}
-        self.merge = merge                  # int32 (n, 4) {seq, first_slot, num_splits, 0}
+    def __init__(self, decode, n_chunks, merge, n_slots, prefill, prefill_merge,
+                 n_prefill_slots):
+        # int32 (n_chunks + n_pieces, 8): chunk records {piece_begin,
+        # piece_end, n_slices, 0..} then piece records {seq, tok_begin,
+        # tok_end, slot_base, slice_begin, q_row, 0, 0}
+        self.decode = decode
+        self.n_chunks = n_chunks
+        self.merge = merge                  # int32 (n, 4) {seq, first_slot, num_partials, 0}
         self.n_slots = n_slots
         self.prefill = prefill              # int32 (n, 8) {seq, q0, q1, kv0, kv1, slot, 0, 0}
         self.prefill_merge = prefill_merge  # int32 (n, 8) {seq, q0, q1, first_slot, splits, ..}
@@ -158,19 +164,25 @@ def plan_tick(
     n = int(q_lens.shape[0])
     group = max(1, num_q_heads // max(1, num_kv_heads))
     tile = max(1, int(lib().hy_prefill_tile_rows()) // group)
-    split_floor = 32 if tokens_per_split <= 0 else max(32, tokens_per_split)
     dec_mask = q_lens == 1
     pre_mask = q_lens > 1
-    dec_cap = int((kv_lens[dec_mask].astype(np.int64) // split_floor + 1).sum()) + 1
+    dec_tokens = int(kv_lens[dec_mask].astype(np.int64).sum())
+    max_chunks = 2 * max(1, num_cus) + 1
+    if tokens_per_split > 0:
+        max_chunks = max(max_chunks, dec_tokens // tokens_per_split + 1)
+    # chunk records + piece records: a piece starts at every chunk boundary
+    # and every sequence; chunks also close at the kernel's piece limit
+    n_dec = int(dec_mask.sum())
+    dec_cap = 2 * (max_chunks + n_dec) + 2
     n_tiles = int(((q_lens[pre_mask].astype(np.int64) + tile - 1) // tile).sum())
     max_steps = int((kv_lens.max() + 63) // 64) if n else 1
     # the planner splits a tile into ranges of at least two 64-key steps
     pre_cap = n_tiles * max(1, max_steps // 2 + 1) + 1
-    dec = np.zeros((dec_cap, 4), dtype=np.int32)
+    dec = np.zeros((dec_cap, 8), dtype=np.int32)
     mrg = np.zeros((n + 1, 4), dtype=np.int32)
     pre = np.zeros((pre_cap, 8), dtype=np.int32)
     pmrg = np.zeros((n_tiles + 1, 8), dtype=np.int32)
-    counts = np.zeros(6, dtype=np.int32)
+    counts = np.zeros(7, dtype=np.int32)
     rc = lib().hy_plan_tick(
         q_lens.ctypes.data, kv_lens.ctypes.data, n, num_q_heads, num_kv_heads,
         page_size, num_cus, tokens_per_split, dec.ctypes.data, dec_cap,
@@ -178,8 +190,9 @@ def plan_tick(
         counts.ctypes.data,
     )
     check(rc, "hy_plan_tick")
-    nd, nm, ns, npf, npm, nps = (int(x) for x in counts)
-    return TickPlan(dec[:nd].copy(), mrg[:nm].copy(), ns, pre[:npf].copy(), pmrg[:npm].copy(), nps)
+    nd, nm, ns, npf, npm, nps, npc = (int(x) for x in counts)
+    return TickPlan(dec[: nd + npc].copy(), nd, mrg[:nm].copy(), ns, pre[:npf].copy(),
+                    pmrg[:npm].copy(), nps)
 
 
 def decode_workspace_bytes(n_slots: int, num_q_heads: int, head_dim: int) -> int:

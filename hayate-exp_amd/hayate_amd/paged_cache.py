@@ -99,7 +99,7 @@ class _DevicePlan:
     def __init__(self, host: "_native.TickPlan", num_q_heads: int, num_kv_heads: int,
                  head_dim: int, device: torch.device):
         self.host = host
-        self.n_decode = len(host.decode)
+        self.n_decode = host.n_chunks
         self.n_merge = len(host.merge)
         self.n_slots = host.n_slots
         self.n_prefill = len(host.prefill)

@@ -118,12 +118,22 @@ int hy_page_scatter(void *pool, int64_t pool_layer_stride,
  * Tick planner (host only, no device access). Given per-sequence query
  * lengths and KV lengths (kv_len = cache_len + q_len), split the work of
  * one attention call into:
- *   decode items  (q_len == 1): int32[n][4] = {seq, tok_begin, tok_end, slot}
- *                 token ranges of equal length (tok_begin a multiple of 32),
- *                 longest first; slot = -1 writes the output directly,
- *                 otherwise the split's partial goes to workspace slot `slot`;
- *   merge items   int32[n][4] = {seq, first_slot, num_splits, 0}, one per
- *                 decode sequence with more than one split;
+ *   decode items  (q_len == 1): int32[n_chunks + n_pieces][8]. The K/V
+ *                 rows of all decode sequences, in sequence order, form one
+ *                 token stream per kv head, cut into n_chunks chunks of
+ *                 equal length (one workgroup each; a cut inside a sequence
+ *                 falls on a multiple of 32 of its tokens). A piece is the
+ *                 part of one sequence inside one chunk. The first n_chunks
+ *                 records are chunks {piece_begin, piece_end, n_slices, and
+ *                 the first piece's seq, tok_begin, tok_end, slot_base,
+ *                 q_row}; the piece records follow: {seq, tok_begin,
+ *                 tok_end, slot_base, slice_begin, q_row, 0, 0}, where
+ *                 slot_base = W * piece index (W partials per piece, one per
+ *                 wave), slice_begin counts 32-token slices from the start
+ *                 of the chunk and q_row is the sequence's packed query row
+ *                 (the prefix sum of q_lens);
+ *   merge items   int32[n][4] = {seq, first_slot, num_partials, 0}, one per
+ *                 decode sequence (all of its pieces' partials);
  *   prefill items (q_len > 1): int32[n][8] =
  *                 {seq, q_begin, q_end, kv_begin, kv_end, slot, 0, 0}:
  *                 query tiles of 256 / G tokens, each over one range of keys
@@ -131,12 +141,14 @@ int hy_page_scatter(void *pool, int64_t pool_layer_stride,
  *                 decode items;
  *   prefill merge items int32[n][8] =
  *                 {seq, q_begin, q_end, first_slot, num_splits, 0, 0, 0}.
- * Split lengths are chosen by simulating the longest-first dispatch of the
- * work onto num_cus CUs. counts_out receives {n_decode, n_merge,
- * n_decode_slots, n_prefill, n_prefill_merge, n_prefill_slots}.
- * Capacities are in items; returns HY_ENOSPACE if one is too small.
- * target_tokens_per_split > 0 fixes the decode split length (rounded up to
- * a multiple of 32) instead.
+ * Decode uses one chunk per CU and kv head (num_cus / num_kv_heads chunks,
+ * at least 256 tokens each); a chunk also ends after as many pieces as the
+ * kernel's query table holds. Prefill split lengths are chosen by
+ * simulating the longest-first dispatch of the work onto num_cus CUs.
+ * counts_out (int32[7]) receives {n_chunks, n_merge, n_decode_slots,
+ * n_prefill, n_prefill_merge, n_prefill_slots, n_pieces}. Capacities are in
+ * items (decode: chunk + piece records); returns HY_ENOSPACE if one is too
+ * small. target_tokens_per_split > 0 sets the decode chunk length instead.
  * Replaces the per-forward metadata of PagedKVCacheManager.begin_batch
  * (paged_cache.py:202-293: page table, cache_lens, kv_lens, block mask).
  */
@@ -156,12 +168,13 @@ int64_t hy_decode_workspace_bytes(int32_t n_slots, int32_t num_q_heads,
 
 /*
  * Paged GQA decode attention for sequences with one query token each
- * (items from hy_plan_tick). Each workgroup covers one decode item and one
- * kv head, loads every K/V row of its token range once and applies it to
- * all num_q_heads / num_kv_heads query heads (QK^T and PV on MFMA).
- * Sequences with several splits leave fp32 partials in the workspace;
+ * (decode items from hy_plan_tick; n_decode = n_chunks). Each workgroup
+ * covers one chunk and one kv head, loads every K/V row of its pieces once
+ * and applies it to all num_q_heads / num_kv_heads query heads (QK^T and
+ * PV on MFMA). Every piece leaves fp32 partials in the workspace;
  * hy_paged_decode_merge, enqueued after this call on the same stream,
- * completes them.
+ * writes the output rows (out and q_start are validated here but written
+ * and read by the merge).
  * Causal semantics: the query of sequence b at position kv_len - 1 sees
  * every key k < kv_len (paged_cache.py:266-271).
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T == 1.

@@ -40,42 +40,81 @@ def plan(q, kv, hq=32, hkv=8, page=128, cus=256, split=0):
     return _native.plan_tick(np.array(q), np.array(kv), hq, hkv, page, cus, split)
 
 
+W = 2  # waves per decode workgroup: partials per piece
+
+
+def chunks_and_pieces(p):
+    return p.decode[: p.n_chunks], p.decode[p.n_chunks :]
+
+
 @pytest.mark.parametrize("split", [0, 96, 256, 1000])
 def test_plan_decode_covers_every_token_once(split):
     rng = np.random.default_rng(0)
     kv = rng.integers(1, 9000, size=40)
     p = plan([1] * 40, kv, split=split)
-    dec = p.decode
     assert len(p.prefill) == 0
-    lengths = dec[:, 2] - dec[:, 1]
-    assert (lengths[:-1] >= lengths[1:]).all()  # longest first
+    chunks, pieces = chunks_and_pieces(p)
+    # chunks own consecutive runs of pieces; slice offsets restart per chunk
+    assert chunks[0, 0] == 0 and chunks[-1, 1] == len(pieces)
+    assert (chunks[1:, 0] == chunks[:-1, 1]).all() and (chunks[:, 1] > chunks[:, 0]).all()
+    nsl = (pieces[:, 2] - pieces[:, 1] + 31) // 32
+    for c in chunks:
+        part = slice(c[0], c[1])
+        assert (pieces[part, 4] == np.concatenate([[0], np.cumsum(nsl[part])[:-1]])).all()
+        assert c[2] == nsl[part].sum()
+    assert (pieces[:, 3] == W * np.arange(len(pieces))).all()
+    # chunk records repeat their first piece
+    first = pieces[chunks[:, 0]]
+    assert (chunks[:, 3:6] == first[:, 0:3]).all() and (chunks[:, 6] == first[:, 3]).all()
+    assert (chunks[:, 7] == first[:, 5]).all()
+    assert (pieces[:, 5] == pieces[:, 0]).all()  # q row of sequence b is b (q_len 1)
     merged = {int(m[0]): m for m in p.merge}
+    assert sorted(merged) == list(range(40))
     for b in range(40):
-        items = dec[dec[:, 0] == b]
-        items = items[np.argsort(items[:, 1])]
-        assert items[0, 1] == 0 and items[-1, 2] == kv[b]
-        assert (items[1:, 1] == items[:-1, 2]).all()
-        assert (items[:, 1] % 32 == 0).all() and (items[:, 2] > items[:, 1]).all()
-        if len(items) == 1:
-            assert items[0, 3] == -1 and b not in merged
-        else:
-            m = merged[b]
-            assert m[2] == len(items)
-            assert (items[:, 3] == np.arange(m[1], m[1] + len(items))).all()
-    assert p.n_slots == int((dec[:, 3] >= 0).sum()) == int(p.merge[:, 2].sum())
+        idx = np.nonzero(pieces[:, 0] == b)[0]
+        rows = pieces[idx]
+        assert (np.diff(idx) == 1).all()
+        assert rows[0, 1] == 0 and rows[-1, 2] == kv[b]
+        assert (rows[1:, 1] == rows[:-1, 2]).all()
+        assert (rows[:, 1] % 32 == 0).all() and (rows[:, 2] > rows[:, 1]).all()
+        m = merged[b]
+        assert m[1] == W * idx[0] and m[2] == W * len(idx)
+    assert p.n_slots == W * len(pieces) == int(p.merge[:, 2].sum())
+    tokens = [int((pieces[c[0]:c[1], 2] - pieces[c[0]:c[1], 1]).sum()) for c in chunks]
+    if split:
+        assert len(chunks) == -(-int(kv.sum()) // split)
+    else:
+        assert len(chunks) == 256 // 8
+    # equal chunks up to the rounding of each cut to 32 tokens (+-16 at
+    # either end)
+    assert max(tokens) - min(tokens) <= 65
 
 
-def test_plan_splits_are_balanced():
+def test_plan_chunk_holds_at_most_the_query_table():
+    # 1000 one-token contexts: chunks close at 32 pieces (G = 4)
+    p = plan([1] * 1000, [1] * 1000)
+    chunks, pieces = chunks_and_pieces(p)
+    assert len(pieces) == 1000
+    assert ((chunks[:, 1] - chunks[:, 0]) <= 32).all()
+    assert chunks[0, 0] == 0 and chunks[-1, 1] == 1000
+    assert (chunks[1:, 0] == chunks[:-1, 1]).all()
+
+
+def test_plan_chunk_cut_rounds_to_32_tokens():
     p = plan([1], [300], split=256)
-    assert sorted(tuple(r[1:3]) for r in p.decode) == [(0, 160), (160, 300)]
+    chunks, pieces = chunks_and_pieces(p)
+    assert [tuple(r[1:3]) for r in pieces] == [(0, 160), (160, 300)]
+    assert [tuple(c[:3]) for c in chunks] == [(0, 1, 5), (1, 2, 5)]
+    assert p.n_slots == 2 * W
 
 
 def test_plan_prefill_tiles_cover_every_query_and_key_once():
     q = [512, 512, 1, 3, 512]
     kv = [512, 4096, 700, 10, 8192]
     p = plan(q, kv)
-    dec, pre = p.decode, p.prefill
-    assert len(dec) >= 1 and (dec[:, 0] == 2).all()
+    _, pieces = chunks_and_pieces(p)
+    pre = p.prefill
+    assert len(pieces) >= 1 and (pieces[:, 0] == 2).all()
     tile = _native.lib().hy_prefill_tile_rows() // 4
     lengths = pre[:, 4] - pre[:, 3]
     assert (lengths[:-1] >= lengths[1:]).all()  # longest first
