@@ -397,9 +397,10 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
   for (int x = cp + 1; x < pe; ++x) flush(pieces[8 * x + 3] + wave);
 }
 
-// Combines the partials of split sequences: grid (merge item, q head),
-// 128 threads (dims). Item = {seq, first_slot, num_splits, 0}. Up to eight
-// splits are loaded in one round of independent loads.
+// Combines the partials of every decode sequence: grid (merge item, q head
+// group of 4), 128 threads = 4 heads x 32 lanes x 4 dims. Item = {seq,
+// first_slot, num_partials, 0}. Up to eight partials are loaded in one
+// round of independent loads.
 __global__ __launch_bounds__(128) void decode_merge_kernel(
     uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ items,
@@ -408,18 +409,22 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(
   const int seq = it[0];
   const int first = it[1];
   const int nsplit = it[2];
-  const int hq = blockIdx.y;
-  const int d = threadIdx.x;
-  float mx = -INFINITY, lsum = 0.f, a = 0.f;
+  const int hq = 4 * blockIdx.y + (threadIdx.x >> 5);
+  const int d = (threadIdx.x & 31) * 4;
+  if (hq >= num_q_heads) return;
+  float mx = -INFINITY, lsum = 0.f;
+  f32x4 a = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < nsplit; s0 += 8) {
-    float m[8], l[8], x[8];
+    float m[8], l[8];
+    f32x4 x[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int64_t base = static_cast<int64_t>(first + s0 + j) * num_q_heads + hq;
       const bool live = s0 + j < nsplit;
       m[j] = live ? ws_ml[base * 2] : -INFINITY;
       l[j] = live ? ws_ml[base * 2 + 1] : 0.f;
-      x[j] = live ? ws_acc[base * kHeadDim + d] : 0.f;
+      x[j] = live ? *reinterpret_cast<const f32x4 *>(ws_acc + base * kHeadDim + d)
+                  : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     float cmx = mx;
 #pragma unroll
@@ -435,8 +440,9 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(
     }
     mx = cmx;
   }
-  out[seq * o_ss + static_cast<int64_t>(q_start[seq]) * o_st + hq * o_sh + d] =
-      static_cast<uint16_t>(f32_to_bf16_rne(a / lsum));
+  uint16_t *dst = out + seq * o_ss + static_cast<int64_t>(q_start[seq]) * o_st + hq * o_sh + d;
+  *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2_rne(a[0] / lsum, a[1] / lsum),
+                                               pack_bf16x2_rne(a[2] / lsum, a[3] / lsum));
 }
 
 template <int G>
@@ -554,7 +560,7 @@ extern "C" int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_
   const float *ws_ml = reinterpret_cast<const float *>(
       static_cast<const char *>(workspace) +
       hy::align256(static_cast<int64_t>(n_slots) * num_q_heads * head_dim * 4));
-  hipLaunchKernelGGL(hy::decode_merge_kernel, dim3(n_merge, num_q_heads), dim3(128), 0,
+  hipLaunchKernelGGL(hy::decode_merge_kernel, dim3(n_merge, (num_q_heads + 3) / 4), dim3(128), 0,
                      static_cast<hipStream_t>(stream), static_cast<uint16_t *>(out),
                      o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items, ws_acc,
                      ws_ml, num_q_heads);

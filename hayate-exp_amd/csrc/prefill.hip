@@ -385,9 +385,10 @@ void prefill_kernel(
   }
 }
 
-// Combines the splits of a query tile: grid (kv head, merge item, 64 groups
-// of 4 rows), 512 threads = 4 rows x 128 dims.
-// Item = {seq, q_begin, q_end, first_slot, num_splits, 0, 0, 0}.
+// Combines the splits of a query tile: grid (kv head, merge item, kRows /
+// 16 row groups), 512 threads = 16 rows x 32 lanes x 4 dims.
+// Item = {seq, q_begin, q_end, first_slot, num_splits, 0, 0, 0}. Up to
+// eight splits are loaded in one round of independent loads.
 template <int G>
 __global__ __launch_bounds__(512) void prefill_merge_kernel(
     uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
@@ -400,25 +401,43 @@ __global__ __launch_bounds__(512) void prefill_merge_kernel(
   const int q_end = it[2];
   const int first = it[3];
   const int nsplit = it[4];
-  const int r = 4 * blockIdx.z + (threadIdx.x >> 7);
-  const int d = threadIdx.x & 127;
+  const int r = 16 * blockIdx.z + (threadIdx.x >> 5);
+  const int d = (threadIdx.x & 31) * 4;
   const int i = q_begin + r / G;
   if (i >= q_end) return;
-  float mx = -INFINITY, lsum = 0.f, a = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const int64_t pr = (static_cast<int64_t>(first + s) * num_kv_heads + kvh) * kRows + r;
-    const float m = ws_ml[pr * 2];
-    if (m == -INFINITY) continue;
-    const float nm = fmaxf(mx, m);
-    const float f_old = mx == -INFINITY ? 0.f : exp2f(mx - nm);
-    const float f_new = exp2f(m - nm);
-    lsum = lsum * f_old + f_new * ws_ml[pr * 2 + 1];
-    a = a * f_old + f_new * ws_acc[pr * kHeadDim + d];
-    mx = nm;
+  float mx = -INFINITY, lsum = 0.f;
+  f32x4 a = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < nsplit; s0 += 8) {
+    float m[8], l[8];
+    f32x4 x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t pr = (static_cast<int64_t>(first + s0 + j) * num_kv_heads + kvh) * kRows + r;
+      const bool live = s0 + j < nsplit;
+      m[j] = live ? ws_ml[pr * 2] : -INFINITY;
+      l[j] = live ? ws_ml[pr * 2 + 1] : 0.f;
+      x[j] = live ? *reinterpret_cast<const f32x4 *>(ws_acc + pr * kHeadDim + d)
+                  : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float cmx = mx;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cmx = fmaxf(cmx, m[j]);
+    if (cmx == -INFINITY) continue;
+    const float f_old = mx == -INFINITY ? 0.f : exp2f(mx - cmx);
+    lsum *= f_old;
+    a *= f_old;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = m[j] == -INFINITY ? 0.f : exp2f(m[j] - cmx);
+      lsum += f * l[j];
+      a += f * x[j];
+    }
+    mx = cmx;
   }
   const int64_t qs = q_start[seq];
-  out[seq * o_ss + (qs + i) * o_st + (kvh * G + r % G) * o_sh + d] =
-      static_cast<uint16_t>(f32_to_bf16_rne(a / lsum));
+  uint16_t *dst = out + seq * o_ss + (qs + i) * o_st + (kvh * G + r % G) * o_sh + d;
+  *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2_rne(a[0] / lsum, a[1] / lsum),
+                                               pack_bf16x2_rne(a[2] / lsum, a[3] / lsum));
 }
 
 template <int G>
@@ -439,7 +458,7 @@ template <int G>
 void launch_prefill_merge(hipStream_t st, int num_kv_heads, int n_merge, uint16_t *out,
                           int64_t o_ss, int64_t o_st, int64_t o_sh, const int32_t *q_start,
                           const int32_t *merge_items, const float *ws_acc, const float *ws_ml) {
-  hipLaunchKernelGGL(prefill_merge_kernel<G>, dim3(num_kv_heads, n_merge, kRows / 4), dim3(512),
+  hipLaunchKernelGGL(prefill_merge_kernel<G>, dim3(num_kv_heads, n_merge, kRows / 16), dim3(512),
                      0, st, out, o_ss, o_st, o_sh, q_start, merge_items, ws_acc, ws_ml,
                      num_kv_heads);
 }
