@@ -47,6 +47,7 @@
 
 #include "decode_shape.h"
 #include "hy_common.h"
+#include "qknorm.h"
 
 namespace hy {
 namespace {
@@ -205,7 +206,7 @@ __device__ __forceinline__ void consume_slice(const SliceRegs &r, const uint16_t
 // read from its record {seq, tok_begin, tok_end, slot_base, slice_begin,
 // q_tok, 0, 0}.
 struct Piece {
-  int seq, t0, t1, slot, sb, qt, nsl;
+  int seq, t0, t1, slot, sb, qt, nsl, ends;
 };
 
 __device__ __forceinline__ Piece load_piece(const int32_t *pieces, int p) {
@@ -217,29 +218,57 @@ __device__ __forceinline__ Piece load_piece(const int32_t *pieces, int p) {
   x.slot = r[3];
   x.sb = r[4];
   x.qt = r[5];
+  x.ends = r[7];
   x.nsl = (x.t1 - x.t0 + kSlice - 1) / kSlice;
   return x;
 }
 
-// Where an issued slice lies: its piece, first token and the piece's end.
+// Where an issued slice lies: its piece, first token and the piece's end;
+// newrow is the slice row of its sequence's query token, or -1.
 struct SliceMeta {
-  int piece, t0, tend;
+  int piece, t0, tend, newrow;
 };
 
-// Two waves per SIMD: the double-buffered slice registers (K, V and the
-// query operand of each slice) need about 240 VGPRs.
-template <int G>
+// Inputs of the fused append (hy_paged_decode_append): the raw q, k, v
+// projections of the step's tokens, the norm weights and rope tables. The
+// kernel's q then points at the raw q rows.
+struct AppendArgs {
+  uint16_t *q_out;
+  int64_t qo_ss, qo_st, qo_sh;
+  const uint16_t *k;
+  int64_t k_ss, k_st, k_sh;
+  const uint16_t *v;
+  int64_t v_ss, v_st, v_sh;
+  const uint16_t *q_w, *k_w;
+  float eps;
+  const float *cos_t, *sin_t;
+  const int32_t *cache_lens;
+};
+
+// Two waves per SIMD: the double-buffered slice registers need about 240
+// VGPRs.
+//
+// kFused: the step's q/k RMSNorm + RoPE + K/V append happens here instead of
+// in a separate launch. The prologue rotates the query rows of the chunk's
+// pieces into the LDS table (the workgroup of a sequence's first piece also
+// writes them to q_out), and for every piece that holds its sequence's new
+// token it builds the new K and V rows of that position and writes them to
+// their page; the workgroup's barrier publishes them before any wave loads
+// that slice (only the one workgroup that owns the row reads it). The
+// values are those of qknorm_rope_append_kernel, bit for bit.
+template <int G, bool kFused>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
-    const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
+    uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool,
     int64_t pool_hs, const int32_t *__restrict__ page_table, int64_t pt_stride,
     const int32_t *__restrict__ items, int n_chunks, float *__restrict__ ws_acc,
-    float *__restrict__ ws_ml, int num_q_heads, int page_shift, float scale_log2) {
-  // One V transpose buffer per wave, and the query rows (G heads) of every
+    float *__restrict__ ws_ml, int num_q_heads, int page_shift, float scale_log2,
+    AppendArgs ap) {
+  // One V transpose buffer per wave and the query rows (G heads) of every
   // piece of the chunk.
+  constexpr int kMaxPieces = decode_max_pieces(G);
   __shared__ __attribute__((aligned(16))) uint16_t sV[kWaves][kSliceElems];
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[kDecodeQTableBytes / 2];
-  constexpr int kMaxPieces = kDecodeQTableBytes / (G * kHeadDim * 2);
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[kMaxPieces * G * kHeadDim];
 
   // Grid (kv head, chunk): heads vary fastest, so with 8 kv heads every
   // XCD streams one head.
@@ -272,14 +301,20 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
   ipc.sb = 0;
   ipc.qt = ch[7];
   ipc.nsl = (ipc.t1 - ipc.t0 + kSlice - 1) / kSlice;
+  ipc.ends = pieces[8 * pb + 7];
   // Loads slice k of the chunk (k-th 32-token slice in piece order) into r.
-  auto issue = [&](SliceRegs &r, SliceMeta &m, int k) {
+  // locate() moves the cursor to slice k and describes it; issue() also
+  // loads it.
+  auto locate = [&](SliceMeta &m, int k) {
     while (k >= ipc.sb + ipc.nsl) ipc = load_piece(pieces, ++ip);
-    const int t0 = ipc.t0 + (k - ipc.sb) * kSlice;
-    issue_slice(r, kh, vh, page_table + ipc.seq * pt_stride, t0, page_shift, lane);
     m.piece = ip;
-    m.t0 = t0;
+    m.t0 = ipc.t0 + (k - ipc.sb) * kSlice;
     m.tend = ipc.t1;
+    m.newrow = ipc.ends && m.t0 + kSlice >= ipc.t1 ? ipc.t1 - 1 - m.t0 : -1;
+  };
+  auto issue = [&](SliceRegs &r, SliceMeta &m, int k) {
+    locate(m, k);
+    issue_slice(r, kh, vh, page_table + ipc.seq * pt_stride, m.t0, page_shift, lane);
   };
 
   // Online-softmax state of the piece being accumulated (cp).
@@ -340,14 +375,22 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
   };
 
   // The first slice's loads go out before the query table is built: all
-  // threads copy the query rows of the chunk's pieces into LDS, 16 bytes
-  // each (the planner keeps a chunk within kMaxPieces pieces).
+  // threads copy (fused: rotate) the query rows of the chunk's pieces into
+  // LDS (the planner keeps a chunk within kMaxPieces pieces). Fused, a first
+  // slice that holds a sequence's new token is loaded only after the
+  // prologue has written that row and the barrier has published it.
   int k = wave;
   SliceRegs ra, rb;
   SliceMeta ma, mb;
-  if (k < n_sl) issue(ra, ma, k);
-  {
-    const int n_p = min(pe - pb, kMaxPieces);
+  bool deferred = false;
+  if (k < n_sl) {
+    locate(ma, k);
+    deferred = kFused && ma.newrow >= 0;
+    if (!deferred)
+      issue_slice(ra, kh, vh, page_table + ipc.seq * pt_stride, ma.t0, page_shift, lane);
+  }
+  const int n_p = min(pe - pb, kMaxPieces);
+  if constexpr (!kFused) {
     for (int idx = threadIdx.x; idx < n_p * G * 16; idx += kWaves * 64) {
       const int j = idx / (G * 16);
       const int h = (idx / 16) % G;
@@ -357,8 +400,54 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
                             (h0 + h) * q_sh + c * 8;
       *reinterpret_cast<u32x4 *>(sQ + (j * G + h) * kHeadDim + c * 8) = load16(src);
     }
+  } else {
+    // One 16-lane group per head row: n_p * G query rows, then one new K/V
+    // row pair per piece (kept only where the piece ends its sequence).
+    const int l16 = threadIdx.x & 15;
+    for (int row = threadIdx.x >> 4; row < n_p * (G + 1); row += kWaves * 4) {
+      const int j = row < n_p * G ? row / G : row - n_p * G;
+      const int32_t *pr = pieces + 8 * (pb + j);
+      const int seq = pr[0];
+      const int pos = pr[6];  // position of the step's token (its cache length)
+      const float *cos_row = ap.cos_t ? ap.cos_t + static_cast<int64_t>(pos) * kHeadDim : nullptr;
+      const float *sin_row = ap.sin_t ? ap.sin_t + static_cast<int64_t>(pos) * kHeadDim : nullptr;
+      if (row < n_p * G) {
+        const int hh = row % G;
+        const int qt = pr[5];
+        float x[8];
+        unpack8(load16(q + seq * q_ss + static_cast<int64_t>(qt) * q_st + (h0 + hh) * q_sh +
+                       l16 * 8),
+                x);
+        if (ap.q_w != nullptr) rms_norm8(x, ap.q_w, l16, ap.eps);
+        if (cos_row != nullptr) rope8(x, cos_row, sin_row, l16);
+        const u32x4 y = pack8_rne(x);
+        *reinterpret_cast<u32x4 *>(sQ + (j * G + hh) * kHeadDim + l16 * 8) = y;
+        if (pr[1] == 0)
+          store16(ap.q_out + seq * ap.qo_ss + static_cast<int64_t>(qt) * ap.qo_st +
+                      (h0 + hh) * ap.qo_sh + l16 * 8,
+                  y);
+      } else {
+        if (pr[7]) {  // the piece holds position pos
+          const int qt = pr[5];
+          float x[8];
+          unpack8(load16(ap.k + seq * ap.k_ss + static_cast<int64_t>(qt) * ap.k_st +
+                         kvh * ap.k_sh + l16 * 8),
+                  x);
+          if (ap.k_w != nullptr) rms_norm8(x, ap.k_w, l16, ap.eps);
+          if (cos_row != nullptr) rope8(x, cos_row, sin_row, l16);
+          const u32x4 yk = pack8_rne(x);
+          const u32x4 yv = load16(ap.v + seq * ap.v_ss + static_cast<int64_t>(qt) * ap.v_st +
+                                  kvh * ap.v_sh + l16 * 8);
+          const int page = page_table[seq * pt_stride + (pos >> page_shift)];
+          const int64_t p = (static_cast<int64_t>(page) << page_shift) + (pos & ((1 << page_shift) - 1));
+          store16(k_pool + kvh * pool_hs + p * kHeadDim + l16 * 8, yk);
+          store16(v_pool + kvh * pool_hs + p * kHeadDim + l16 * 8, yv);
+        }
+      }
+    }
   }
   __syncthreads();
+  if (deferred) issue_slice(ra, kh, vh, page_table + ipc.seq * pt_stride, ma.t0, page_shift, lane);
   load_q(pb);
 
   // Wave w takes slices w, w + 4, ... of the chunk. Double-buffered: the
@@ -445,15 +534,15 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(
                                                pack_bf16x2_rne(a[2] / lsum, a[3] / lsum));
 }
 
-template <int G>
+template <int G, bool kFused>
 void launch_decode(hipStream_t st, dim3 grid, const uint16_t *q, int64_t q_ss, int64_t q_st,
-                   int64_t q_sh, const uint16_t *k_pool, const uint16_t *v_pool, int64_t pool_hs,
+                   int64_t q_sh, uint16_t *k_pool, uint16_t *v_pool, int64_t pool_hs,
                    const int32_t *page_table, int64_t pt_stride, const int32_t *items,
                    int n_chunks, float *ws_acc, float *ws_ml, int num_q_heads, int page_shift,
-                   float scale_log2) {
-  hipLaunchKernelGGL(decode_kernel<G>, grid, dim3(kWaves * 64), 0, st, q, q_ss, q_st, q_sh, k_pool,
-                     v_pool, pool_hs, page_table, pt_stride, items, n_chunks, ws_acc, ws_ml,
-                     num_q_heads, page_shift, scale_log2);
+                   float scale_log2, const AppendArgs &ap) {
+  hipLaunchKernelGGL((decode_kernel<G, kFused>), grid, dim3(kWaves * 64), 0, st, q, q_ss, q_st,
+                     q_sh, k_pool, v_pool, pool_hs, page_table, pt_stride, items, n_chunks, ws_acc,
+                     ws_ml, num_q_heads, page_shift, scale_log2, ap);
 }
 
 // Workspace layout: [acc fp32 n_slots*Hq*D][max,sum fp32 n_slots*Hq*2],
@@ -472,16 +561,18 @@ extern "C" int64_t hy_decode_workspace_bytes(int32_t n_slots, int32_t num_q_head
          hy::align256(static_cast<int64_t>(n_slots) * num_q_heads * 2 * 4);
 }
 
-extern "C" int hy_paged_decode(
-    const void *q, int64_t q_stride_seq, int64_t q_stride_tok, int64_t q_stride_head,
-    void *out, int64_t o_stride_seq, int64_t o_stride_tok, int64_t o_stride_head,
-    const void *k_pool, const void *v_pool, int64_t pool_head_stride,
-    const int32_t *page_table, int64_t page_table_stride, const int32_t *q_start,
-    const int32_t *decode_items, int32_t n_decode, int32_t n_slots, void *workspace,
-    int64_t workspace_bytes,
-    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-    int32_t page_size, float scale, void *stream) {
-  hy::clear_error();
+namespace {
+
+// Shared by hy_paged_decode and hy_paged_decode_append: validation and the
+// launch over the chunk grid.
+int paged_decode_impl(const char *name, const void *q, int64_t q_stride_seq,
+                      int64_t q_stride_tok, int64_t q_stride_head, void *out, const void *k_pool,
+                      const void *v_pool, int64_t pool_head_stride, const int32_t *page_table,
+                      int64_t page_table_stride, const int32_t *q_start,
+                      const int32_t *decode_items, int32_t n_decode, int32_t n_slots,
+                      void *workspace, int64_t workspace_bytes, int32_t num_seqs,
+                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t page_size, float scale, void *stream, const hy::AppendArgs *ap) {
   HY_REQUIRE(num_seqs >= 1, "num_seqs must be positive");
   HY_REQUIRE(scale > 0.f, "softmax scale must be positive");
   HY_REQUIRE(num_kv_heads >= 1 && num_q_heads >= num_kv_heads &&
@@ -495,7 +586,7 @@ extern "C" int hy_paged_decode(
   HY_REQUIRE(n_decode >= 0 && n_slots >= 0, "item counts must be non-negative");
   if (n_decode == 0) return HY_OK;
   HY_REQUIRE(q && out && k_pool && v_pool && page_table && q_start && decode_items,
-             "hy_paged_decode: null pointer argument");
+             "%s: null pointer argument", name);
   const int G = num_q_heads / num_kv_heads;
   HY_REQUIRE_SUPPORTED(G == 1 || G == 2 || G == 4 || G == 8 || G == 16,
                        "GQA group size %d unsupported (1, 2, 4, 8, 16)", G);
@@ -515,13 +606,21 @@ extern "C" int hy_paged_decode(
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid(num_kv_heads, n_decode);
   const uint16_t *qq = static_cast<const uint16_t *>(q);
-  const uint16_t *kp = static_cast<const uint16_t *>(k_pool);
-  const uint16_t *vp = static_cast<const uint16_t *>(v_pool);
-#define HY_DECODE_CASE(GG)                                                                    \
-  case GG:                                                                                    \
-    hy::launch_decode<GG>(st, grid, qq, q_stride_seq, q_stride_tok, q_stride_head, kp, vp,    \
-                          pool_head_stride, page_table, page_table_stride, decode_items,      \
-                          n_decode, ws_acc, ws_ml, num_q_heads, page_shift, scale_log2);      \
+  uint16_t *kp = static_cast<uint16_t *>(const_cast<void *>(k_pool));
+  uint16_t *vp = static_cast<uint16_t *>(const_cast<void *>(v_pool));
+  const hy::AppendArgs none{};
+#define HY_DECODE_CASE(GG)                                                                     \
+  case GG:                                                                                     \
+    if (ap)                                                                                    \
+      hy::launch_decode<GG, true>(st, grid, qq, q_stride_seq, q_stride_tok, q_stride_head, kp, \
+                                  vp, pool_head_stride, page_table, page_table_stride,         \
+                                  decode_items, n_decode, ws_acc, ws_ml, num_q_heads,          \
+                                  page_shift, scale_log2, *ap);                                \
+    else                                                                                       \
+      hy::launch_decode<GG, false>(st, grid, qq, q_stride_seq, q_stride_tok, q_stride_head,    \
+                                   kp, vp, pool_head_stride, page_table, page_table_stride,    \
+                                   decode_items, n_decode, ws_acc, ws_ml, num_q_heads,         \
+                                   page_shift, scale_log2, none);                              \
     break;
   switch (G) {
     HY_DECODE_CASE(1)
@@ -529,12 +628,75 @@ extern "C" int hy_paged_decode(
     HY_DECODE_CASE(4)
     HY_DECODE_CASE(8)
     HY_DECODE_CASE(16)
-    default:
-      hy::set_error("GQA group size %d unsupported (1, 2, 4, 8, 16)", G);
-      return HY_EUNSUPPORTED;
   }
 #undef HY_DECODE_CASE
-  return hy::launch_status("hy_paged_decode");
+  return hy::launch_status(name);
+}
+
+}  // namespace
+
+extern "C" int hy_paged_decode(
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok, int64_t q_stride_head,
+    void *out, int64_t o_stride_seq, int64_t o_stride_tok, int64_t o_stride_head,
+    const void *k_pool, const void *v_pool, int64_t pool_head_stride,
+    const int32_t *page_table, int64_t page_table_stride, const int32_t *q_start,
+    const int32_t *decode_items, int32_t n_decode, int32_t n_slots, void *workspace,
+    int64_t workspace_bytes,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t page_size, float scale, void *stream) {
+  hy::clear_error();
+  (void)o_stride_seq;
+  (void)o_stride_tok;
+  (void)o_stride_head;
+  return paged_decode_impl("hy_paged_decode", q, q_stride_seq, q_stride_tok, q_stride_head, out,
+                           k_pool, v_pool, pool_head_stride, page_table, page_table_stride,
+                           q_start, decode_items, n_decode, n_slots, workspace, workspace_bytes,
+                           num_seqs, num_q_heads, num_kv_heads, head_dim, page_size, scale,
+                           stream, nullptr);
+}
+
+extern "C" int hy_paged_decode_append(
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok, int64_t q_stride_head,
+    void *q_out, int64_t qo_stride_seq, int64_t qo_stride_tok, int64_t qo_stride_head,
+    const void *k, int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
+    const void *v, int64_t v_stride_seq, int64_t v_stride_tok, int64_t v_stride_head,
+    const void *q_norm_weight, const void *k_norm_weight, float eps, const float *cos_table,
+    const float *sin_table, int32_t max_positions, void *out, void *k_pool, void *v_pool,
+    int64_t pool_head_stride, const int32_t *page_table, int64_t page_table_stride,
+    const int32_t *q_start, const int32_t *cache_lens, const int32_t *decode_items,
+    int32_t n_decode, int32_t n_slots, void *workspace, int64_t workspace_bytes,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t page_size, float scale, void *stream) {
+  hy::clear_error();
+  HY_REQUIRE(q_out && k && v && cache_lens, "hy_paged_decode_append: null pointer argument");
+  HY_REQUIRE((cos_table == nullptr) == (sin_table == nullptr),
+             "cos_table and sin_table must both be given or both be NULL");
+  HY_REQUIRE(cos_table == nullptr || max_positions > 0,
+             "max_positions must be positive when tables are given");
+  hy::AppendArgs ap;
+  ap.q_out = static_cast<uint16_t *>(q_out);
+  ap.qo_ss = qo_stride_seq;
+  ap.qo_st = qo_stride_tok;
+  ap.qo_sh = qo_stride_head;
+  ap.k = static_cast<const uint16_t *>(k);
+  ap.k_ss = k_stride_seq;
+  ap.k_st = k_stride_tok;
+  ap.k_sh = k_stride_head;
+  ap.v = static_cast<const uint16_t *>(v);
+  ap.v_ss = v_stride_seq;
+  ap.v_st = v_stride_tok;
+  ap.v_sh = v_stride_head;
+  ap.q_w = static_cast<const uint16_t *>(q_norm_weight);
+  ap.k_w = static_cast<const uint16_t *>(k_norm_weight);
+  ap.eps = eps;
+  ap.cos_t = cos_table;
+  ap.sin_t = sin_table;
+  ap.cache_lens = cache_lens;
+  return paged_decode_impl("hy_paged_decode_append", q, q_stride_seq, q_stride_tok,
+                           q_stride_head, out, k_pool, v_pool, pool_head_stride, page_table,
+                           page_table_stride, q_start, decode_items, n_decode, n_slots,
+                           workspace, workspace_bytes, num_seqs, num_q_heads, num_kv_heads,
+                           head_dim, page_size, scale, stream, &ap);
 }
 
 extern "C" int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,

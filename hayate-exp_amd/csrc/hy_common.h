@@ -103,8 +103,7 @@ __device__ __forceinline__ float row16_sum(float x) {
 }
 
 // Sequence index owning packed token `tok` given cumulative q_start[0..n].
-__device__ __forceinline__ int find_seq(const int32_t *__restrict__ q_start,
-                                        int num_seqs, int tok) {
+__device__ __forceinline__ int find_seq(const int32_t *q_start, int num_seqs, int tok) {
   int lo = 0, hi = num_seqs - 1;
   while (lo < hi) {
     int mid = (lo + hi + 1) >> 1;

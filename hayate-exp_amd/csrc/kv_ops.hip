@@ -2,8 +2,8 @@
 //
 // Work decomposition: one 16-lane row group per 128-element head row; every
 // lane moves 8 bf16 (16 bytes), so a wave covers four head rows with fully
-// coalesced 256-byte row segments. These kernels are HBM-bound copies; no
-// LDS is used.
+// coalesced 256-byte row segments. These kernels are HBM-bound copies; the
+// append kernels keep only the batch's q_start / cache_lens in LDS.
 //
 // Built with -ffp-contract=off: the norm and rotation must round each fp32
 // product and sum separately, as the reference's chain of elementwise torch
@@ -13,12 +13,53 @@
 #include <stdio.h>
 
 #include "hy_common.h"
+#include "qknorm.h"
 
 namespace hy {
 
 namespace {
 
 constexpr int kRowsPerBlock = 16;  // 256 threads = 16 head rows
+constexpr int kLdsSeqs = 1024;     // batches up to this size stage their metadata in LDS
+
+// Per-block copy of q_start and cache_lens in LDS: the token -> sequence
+// search and the position lookup then cost LDS reads instead of a chain of
+// dependent global loads (one per binary-search step). Larger batches read
+// global memory directly.
+struct TokPos {
+  int seq, pos;  // sequence of the token and its position in that sequence
+};
+
+struct SeqMeta {
+  const int32_t *s_qs, *s_cl;  // LDS copies (valid when staged)
+  const int32_t *q_start, *cache_lens;
+  int num_seqs;
+  bool staged;
+
+  __device__ __forceinline__ TokPos locate(int tok) const {
+    if (staged) {
+      const int b = find_seq(s_qs, num_seqs, tok);
+      return {b, s_cl[b] + tok - s_qs[b]};
+    }
+    const int b = find_seq(q_start, num_seqs, tok);
+    return {b, cache_lens[b] + tok - q_start[b]};
+  }
+};
+
+__device__ __forceinline__ SeqMeta stage_seq_meta(int32_t *s_qs, int32_t *s_cl,
+                                                 const int32_t *__restrict__ q_start,
+                                                 const int32_t *__restrict__ cache_lens,
+                                                 int num_seqs) {
+  const bool staged = num_seqs <= kLdsSeqs;
+  if (staged) {
+    for (int j = threadIdx.x; j <= num_seqs; j += blockDim.x) {
+      s_qs[j] = q_start[j];
+      if (j < num_seqs) s_cl[j] = cache_lens[j];
+    }
+    __syncthreads();
+  }
+  return {s_qs, s_cl, q_start, cache_lens, num_seqs, staged};
+}
 
 struct RowAddr {
   int64_t seq, tok, head;
@@ -44,6 +85,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     const int32_t *__restrict__ cache_lens,
     const int32_t *__restrict__ page_table, int64_t pt_stride, int num_seqs,
     int total_tokens, int num_kv_heads, int page_size) {
+  __shared__ int32_t s_qs[kLdsSeqs + 1];
+  __shared__ int32_t s_cl[kLdsSeqs];
+  const SeqMeta meta = stage_seq_meta(s_qs, s_cl, q_start, cache_lens, num_seqs);
   const int lane = threadIdx.x & 15;
   const int64_t rows_per_kind = static_cast<int64_t>(total_tokens) * num_kv_heads;
   const int64_t row =
@@ -53,9 +97,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
   const int64_t r = is_v ? row - rows_per_kind : row;
   const int tok = static_cast<int>(r / num_kv_heads);
   const int h = static_cast<int>(r % num_kv_heads);
-  const int b = find_seq(q_start, num_seqs, tok);
-  const int i = tok - q_start[b];
-  const int pos = cache_lens[b] + i;
+  const TokPos tp = meta.locate(tok);
+  const int b = tp.seq;
+  const int pos = tp.pos;
   const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);
 
   const uint16_t *src = is_v ? v + b * v_ss + static_cast<int64_t>(tok) * v_st + h * v_sh
@@ -68,83 +112,6 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 // Fused q/k RMSNorm + RoPE + K/V append.
 // Row index r over [q rows | k rows | v rows], each kind token-major.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void unpack8(const u32x4 w, float (&x)[8]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    x[2 * j] = bf16_lo(w[j]);
-    x[2 * j + 1] = bf16_hi(w[j]);
-  }
-}
-
-__device__ __forceinline__ u32x4 pack8_rne(const float (&y)[8]) {
-  u32x4 w;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2_rne(y[2 * j], y[2 * j + 1]);
-  return w;
-}
-
-// x' = bf16((x * rsqrt(mean(x^2) + eps)) * w), fp32 arithmetic, per head row
-// held by 16 lanes x 8 elements (torch/_decomp/decompositions.py
-// _fused_rms_norm: upcast, pow 2, mean, add eps, rsqrt, mul, mul weight,
-// cast back).
-// The squares of bf16 values are exact and so is their fp64 sum, so the
-// mean is the correctly rounded one whatever the reduction order. sqrt and
-// the reciprocal are taken in fp64 and rounded to fp32, which equals the
-// correctly rounded fp32 operation (53 >= 2 * 24 + 2 makes the double
-// rounding innocuous for both), independent of fp32 sqrt/div lowering.
-__device__ __forceinline__ double row16_sum_f64(double x) {
-  x += __shfl_xor(x, 8, 16);
-  x += __shfl_xor(x, 4, 16);
-  x += __shfl_xor(x, 2, 16);
-  x += __shfl_xor(x, 1, 16);
-  return x;
-}
-
-__device__ __forceinline__ void rms_norm8(float (&x)[8],
-                                          const uint16_t *__restrict__ w,
-                                          int lane, float eps) {
-  double ss = 0.0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ss += static_cast<double>(x[j] * x[j]);
-  ss = row16_sum_f64(ss);
-  const float mean = static_cast<float>(ss) * (1.0f / kHeadDim);
-  const float root = static_cast<float>(sqrt(static_cast<double>(mean + eps)));
-  const float rstd = static_cast<float>(1.0 / static_cast<double>(root));
-  const u32x4 wv = load16(w + lane * 8);
-  float wf[8];
-  unpack8(wv, wf);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float y = (x[j] * rstd) * wf[j];
-    x[j] = bf16_to_f32(static_cast<uint16_t>(f32_to_bf16_rne(y)));
-  }
-}
-
-// y = bf16(x * cos + rotate_half(x) * sin), rotate_half(x) = cat(-x2, x1)
-// (hayate/model/rope.py:31-47). Lane l holds features 8l..8l+7; its partner
-// l ^ 8 holds the other half.
-__device__ __forceinline__ void rope8(float (&x)[8],
-                                      const float *__restrict__ cos_row,
-                                      const float *__restrict__ sin_row,
-                                      int lane) {
-  float other[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) other[j] = __shfl_xor(x[j], 8, 16);
-  const float sgn = lane < 8 ? -1.0f : 1.0f;
-  const f32x4 c0 = *reinterpret_cast<const f32x4 *>(cos_row + lane * 8);
-  const f32x4 c1 = *reinterpret_cast<const f32x4 *>(cos_row + lane * 8 + 4);
-  const f32x4 s0 = *reinterpret_cast<const f32x4 *>(sin_row + lane * 8);
-  const f32x4 s1 = *reinterpret_cast<const f32x4 *>(sin_row + lane * 8 + 4);
-  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-  const float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float a = x[j] * c[j];
-    const float r = (sgn * other[j]) * s[j];
-    x[j] = a + r;
-  }
-}
-
 __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
     uint16_t *__restrict__ q_out, int64_t qo_ss, int64_t qo_st, int64_t qo_sh,
@@ -157,6 +124,9 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ cache_lens,
     const int32_t *__restrict__ page_table, int64_t pt_stride, int num_seqs,
     int total_tokens, int num_q_heads, int num_kv_heads, int page_size) {
+  __shared__ int32_t s_qs[kLdsSeqs + 1];
+  __shared__ int32_t s_cl[kLdsSeqs];
+  const SeqMeta meta = stage_seq_meta(s_qs, s_cl, q_start, cache_lens, num_seqs);
   const int lane = threadIdx.x & 15;
   const int64_t nq = static_cast<int64_t>(total_tokens) * num_q_heads;
   const int64_t nk = static_cast<int64_t>(total_tokens) * num_kv_heads;
@@ -176,9 +146,9 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
   }
   const int tok = static_cast<int>(r / heads);
   const int h = static_cast<int>(r % heads);
-  const int b = find_seq(q_start, num_seqs, tok);
-  const int i = tok - q_start[b];
-  const int pos = cache_lens[b] + i;
+  const TokPos tp = meta.locate(tok);
+  const int b = tp.seq;
+  const int pos = tp.pos;
 
   if (kind == 2) {
     const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);

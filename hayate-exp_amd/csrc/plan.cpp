@@ -227,7 +227,8 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
     it[3] = kDecodeWaves * i;
     it[4] = pieces[i].slice_begin;
     it[5] = q_begin[pieces[i].seq];
-    it[6] = it[7] = 0;
+    it[6] = kv_lens[pieces[i].seq] - 1;  // position of the sequence's query token
+    it[7] = pieces[i].t1 == kv_lens[pieces[i].seq];  // the piece holds that token
   }
 
   // Prefill: query tiles of kPrefillRows / G tokens; the key range of a tile is

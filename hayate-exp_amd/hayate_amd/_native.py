@@ -65,6 +65,12 @@ _SIGNATURES = {
          _P, _P, _I32, _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P],
         ctypes.c_int,
     ),
+    "hy_paged_decode_append": (
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64,
+         _I64, _P, _P, _F32, _P, _P, _I32, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _I32,
+         _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P],
+        ctypes.c_int,
+    ),
     "hy_paged_decode_merge": (
         [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P, _I64, _I32, _I32, _P],
         ctypes.c_int,

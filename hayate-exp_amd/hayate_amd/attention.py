@@ -61,10 +61,22 @@ class GroupedQueryAttention(nn.Module):
             # Varlen ticks carry packed tokens: x is (1, N, d_in).
             if B != 1:
                 raise ValueError("a varlen tick expects x of shape (1, tokens, d_in)")
-            q_rot = paged_cache.norm_rope_write_layer(
-                layer_idx, q[0], k[0], v[0], q_norm_w, k_norm_w, eps, cos, sin
+            if all(ql == 1 for ql in paged_cache.q_lens):
+                # a decode tick: norm, rope, append and attention in one launch
+                _, context = paged_cache.decode_layer(
+                    layer_idx, q[0], k[0], v[0], q_norm_w, k_norm_w, eps, cos, sin
+                )
+            else:
+                q_rot = paged_cache.norm_rope_write_layer(
+                    layer_idx, q[0], k[0], v[0], q_norm_w, k_norm_w, eps, cos, sin
+                )
+                context = paged_cache.attend_layer(q_rot, layer_idx)
+            context = context.unsqueeze(0)
+        elif T == 1:
+            _, context = paged_cache.decode_layer(
+                layer_idx, q, k, v, q_norm_w, k_norm_w, eps, cos, sin
             )
-            context = paged_cache.attend_layer(q_rot, layer_idx).unsqueeze(0)
+            context = context.transpose(1, 2)
         else:
             q_rot = paged_cache.norm_rope_write_layer(
                 layer_idx, q, k, v, q_norm_w, k_norm_w, eps, cos, sin

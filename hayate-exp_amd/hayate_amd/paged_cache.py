@@ -93,6 +93,16 @@ def _aligned_rows(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous() if acc & 7 else t
 
 
+@dataclass
+class _AppendInputs:
+    q: torch.Tensor
+    q_out: torch.Tensor
+    num_q_heads: int
+    keep: tuple  # tensors whose addresses are in head / tables
+    head: tuple  # q .. k_norm_weight arguments of the C call
+    tables: tuple  # cos, sin, max_positions
+
+
 class _DevicePlan:
     """One tick's work lists on the device plus the split workspaces."""
 
@@ -304,7 +314,24 @@ class PagedKVBatch:
         outputs, (B, T, H, D) (or packed (N, H, D) for a varlen tick); positions
         are cache_lens + token index. Returns the rotated q in the same
         layout; k and v go to the pool only."""
-        _require_hip(q, "norm_rope_write_layer")
+        a = self._append_inputs("norm_rope_write_layer", q, k, v, q_norm_weight,
+                                k_norm_weight, cos, sin)
+        k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
+        rc = _native.lib().hy_qknorm_rope_append(
+            *a.head, float(eps), *a.tables,
+            k_ptr, v_ptr, hs,
+            self._q_start_ptr, self._cache_lens_ptr, self._pt_ptr, self._pt_stride,
+            self.num_seqs, self.total_tokens, a.num_q_heads, self.num_kv_heads,
+            self.head_dim, self.page_size, _stream_handle(self.device),
+        )
+        _native.check(rc, "hy_qknorm_rope_append")
+        return a.q_out
+
+    def _append_inputs(self, what, q, k, v, q_norm_weight, k_norm_weight, cos, sin):
+        """Checked, 16-byte-aligned inputs of the fused norm + rope + append
+        and the C arguments they map to (shared by norm_rope_write_layer and
+        decode_layer)."""
+        _require_hip(q, what)
         q = _aligned_rows(q)
         k = _aligned_rows(k)
         v = _aligned_rows(v)
@@ -335,21 +362,72 @@ class PagedKVBatch:
         for w in (qw, kw):
             if w is not None and (w.dtype != torch.bfloat16 or w.numel() != self.head_dim):
                 raise TypeError("norm weights must be bfloat16 (head_dim,)")
-        k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
-        rc = _native.lib().hy_qknorm_rope_append(
-            q.data_ptr(), *qs, q_out.data_ptr(), *qos,
-            k.data_ptr(), *ks, v.data_ptr(), *vs,
-            None if qw is None else qw.data_ptr(),
-            None if kw is None else kw.data_ptr(), float(eps),
-            None if cos is None else cos.data_ptr(),
-            None if sin is None else sin.data_ptr(), max_pos,
-            k_ptr, v_ptr, hs,
-            self._q_start_ptr, self._cache_lens_ptr, self._pt_ptr, self._pt_stride,
-            self.num_seqs, self.total_tokens, num_q_heads, self.num_kv_heads,
-            self.head_dim, self.page_size, _stream_handle(self.device),
+        return _AppendInputs(
+            q=q, q_out=q_out, num_q_heads=num_q_heads, keep=(k, v, qw, kw, cos, sin),
+            head=(q.data_ptr(), *qs, q_out.data_ptr(), *qos, k.data_ptr(), *ks,
+                  v.data_ptr(), *vs, None if qw is None else qw.data_ptr(),
+                  None if kw is None else kw.data_ptr()),
+            tables=(None if cos is None else cos.data_ptr(),
+                    None if sin is None else sin.data_ptr(), max_pos),
         )
-        _native.check(rc, "hy_qknorm_rope_append")
-        return q_out
+
+    def decode_layer(
+        self,
+        layer_idx: int,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        q_norm_weight: Optional[torch.Tensor],
+        k_norm_weight: Optional[torch.Tensor],
+        eps: float,
+        cos: Optional[torch.Tensor],
+        sin: Optional[torch.Tensor],
+        scale: Optional[float] = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """norm_rope_write_layer then attend_layer, for a batch whose
+        sequences all decode one token, in one kernel launch plus the merge
+        (attention.py:62-75 then paged_cache.py:62-71). Inputs as for
+        norm_rope_write_layer; returns (q_rot, out) exactly as the two calls
+        would: q_rot in the input layout, out as attend_layer returns it.
+        Pool contents and q_rot are bit-identical to the two-call path."""
+        if any(ql != 1 for ql in self.q_lens):
+            raise ValueError("decode_layer needs q_len == 1 for every sequence")
+        a = self._append_inputs("decode_layer", q, k, v, q_norm_weight, k_norm_weight, cos,
+                                sin)
+        num_q_heads = a.num_q_heads
+        if num_q_heads % self.num_kv_heads:
+            raise ValueError("query heads must be a multiple of kv heads")
+        if self.varlen:
+            out = torch.empty((self.total_tokens, num_q_heads, self.head_dim),
+                              dtype=q.dtype, device=q.device)
+            result = out
+            os_ = self._layout(out, "thd")
+        else:
+            B, T = self.num_seqs, self.query_len
+            buf = torch.empty((B, T, num_q_heads, self.head_dim), dtype=q.dtype,
+                              device=q.device)
+            result = buf.transpose(1, 2)
+            os_ = self._layout(result, "bhtd")
+        if scale is None:
+            scale = 1.0 / math.sqrt(self.head_dim)
+        plan = self.plan(num_q_heads)
+        k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
+        stream = _stream_handle(self.device)
+        lib = _native.lib()
+        self._launch("hy_paged_decode_append", lib.hy_paged_decode_append,
+            *a.head, float(eps), *a.tables, result.data_ptr(), k_ptr, v_ptr, hs,
+            self._pt_ptr, self._pt_stride, self._q_start_ptr, self._cache_lens_ptr,
+            plan.decode_ptr, plan.n_decode, plan.n_slots, plan.workspace_ptr,
+            plan.workspace_bytes, self.num_seqs, num_q_heads, self.num_kv_heads,
+            self.head_dim, self.page_size, float(scale), stream,
+        )
+        self._launch("hy_paged_decode_merge", lib.hy_paged_decode_merge,
+            result.data_ptr(), *os_, self._q_start_ptr,
+            plan.merge_ptr, plan.n_merge, plan.n_slots,
+            plan.workspace_ptr, plan.workspace_bytes, num_q_heads,
+            self.head_dim, stream,
+        )
+        return a.q_out, result
 
     def _check_kv(self, k: torch.Tensor, v: torch.Tensor, head_axis: int) -> None:
         if k.shape != v.shape:

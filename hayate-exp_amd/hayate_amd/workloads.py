@@ -155,11 +155,16 @@ def fill_pool(manager: PagedKVCacheManager, seed: int) -> None:
 
 def make_workload(name: str, device: torch.device | str = "cuda", num_layers: int = 1,
                   pool_tokens: Optional[int] = None, seed: Optional[int] = None,
-                  fill: bool = True, tokens_per_split: int = 0) -> Workload:
+                  fill: bool = True, tokens_per_split: int = 0,
+                  lengths: Optional[tuple[list[int], list[int]]] = None) -> Workload:
+    """The named configuration; `lengths` = (cache_lens, q_lens) replaces its
+    request lengths (same pool, seed and placement rule)."""
     spec = SPECS[name]
     seed = spec.seed if seed is None else seed
     gen = torch.Generator().manual_seed(seed)
     cache_lens, q_lens = _lengths(name, gen)
+    if lengths is not None:
+        cache_lens, q_lens = list(lengths[0]), list(lengths[1])
     pool_tokens = pool_tokens or spec.pool_tokens
     n_pages_pool = pool_tokens // PAGE
     manager = PagedKVCacheManager(

@@ -127,11 +127,13 @@ int hy_page_scatter(void *pool, int64_t pool_layer_stride,
  *                 records are chunks {piece_begin, piece_end, n_slices, and
  *                 the first piece's seq, tok_begin, tok_end, slot_base,
  *                 q_row}; the piece records follow: {seq, tok_begin,
- *                 tok_end, slot_base, slice_begin, q_row, 0, 0}, where
+ *                 tok_end, slot_base, slice_begin, q_row, q_pos, ends}, where
  *                 slot_base = W * piece index (W partials per piece, one per
  *                 wave), slice_begin counts 32-token slices from the start
- *                 of the chunk and q_row is the sequence's packed query row
- *                 (the prefix sum of q_lens);
+ *                 of the chunk, q_row is the sequence's packed query row
+ *                 (the prefix sum of q_lens), q_pos = kv_len - 1 the
+ *                 position of its query token and ends = 1 for the piece
+ *                 that holds that position;
  *   merge items   int32[n][4] = {seq, first_slot, num_partials, 0}, one per
  *                 decode sequence (all of its pieces' partials);
  *   prefill items (q_len > 1): int32[n][8] =
@@ -190,6 +192,36 @@ int hy_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
                     int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
                     int32_t head_dim, int32_t page_size, float scale,
                     void *stream);
+
+/*
+ * hy_qknorm_rope_append fused into hy_paged_decode for a batch whose
+ * sequences all have q_len == 1 (every sequence's token is appended at
+ * position cache_lens[b] and attends to keys 0 .. cache_lens[b]). q, k, v
+ * are the raw projections with the strides of hy_qknorm_rope_append; the
+ * rotated q rows are written to q_out, the new K and V rows to their pages,
+ * bit-identical to hy_qknorm_rope_append, and the attention partials to the
+ * workspace as hy_paged_decode does (hy_paged_decode_merge then writes out).
+ * One launch instead of two per decode layer: the workgroups rotate the
+ * query rows of their pieces themselves and take the new token's K/V row
+ * from LDS, so no workgroup waits for another's write.
+ * Replaces the decode case of attention.py:62-75 (norm, rope, write_layer)
+ * followed by paged_cache.py:62-71 (attend_layer).
+ */
+int hy_paged_decode_append(
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
+    int64_t q_stride_head, void *q_out, int64_t qo_stride_seq,
+    int64_t qo_stride_tok, int64_t qo_stride_head, const void *k,
+    int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
+    const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
+    int64_t v_stride_head, const void *q_norm_weight,
+    const void *k_norm_weight, float eps, const float *cos_table,
+    const float *sin_table, int32_t max_positions, void *out, void *k_pool,
+    void *v_pool, int64_t pool_head_stride, const int32_t *page_table,
+    int64_t page_table_stride, const int32_t *q_start,
+    const int32_t *cache_lens, const int32_t *decode_items, int32_t n_decode,
+    int32_t n_slots, void *workspace, int64_t workspace_bytes,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t page_size, float scale, void *stream);
 
 /*
  * Merge of split decode partials (log-sum-exp over the splits of each

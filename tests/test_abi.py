@@ -68,6 +68,8 @@ def test_plan_decode_covers_every_token_once(split):
     assert (chunks[:, 3:6] == first[:, 0:3]).all() and (chunks[:, 6] == first[:, 3]).all()
     assert (chunks[:, 7] == first[:, 5]).all()
     assert (pieces[:, 5] == pieces[:, 0]).all()  # q row of sequence b is b (q_len 1)
+    assert (pieces[:, 6] == kv[pieces[:, 0]] - 1).all()  # position of the query token
+    assert (pieces[:, 7] == (pieces[:, 2] == kv[pieces[:, 0]])).all()  # holds that token
     merged = {int(m[0]): m for m in p.merge}
     assert sorted(merged) == list(range(40))
     for b in range(40):

@@ -285,3 +285,85 @@ def test_graph_replay_matches_eager():
         torch.cuda.synchronize()
         assert np.array_equal(bits(q_g), q_eager), f"replay {rep}: rotated q differs"
         assert np.array_equal(bits(out_g), out_eager), f"replay {rep}: attention differs"
+
+
+def _fused_vs_two_calls(w_a, w_b, layer=0):
+    """decode_layer on w_a's pool, norm_rope_write_layer + attend_layer on
+    w_b's identical pool: rotated q, pool and attention output must match
+    bit for bit."""
+    ba = w_a.begin()
+    q_f, out_f = ba.decode_layer(layer, w_a.q, w_a.k, w_a.v, w_a.q_norm_w, w_a.k_norm_w, EPS,
+                                 w_a.cos, w_a.sin)
+    bb = w_b.begin()
+    q_s = bb.norm_rope_write_layer(layer, w_b.q, w_b.k, w_b.v, w_b.q_norm_w, w_b.k_norm_w, EPS,
+                                   w_b.cos, w_b.sin)
+    out_s = bb.attend_layer(q_s, layer)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(q_f), bits(q_s)), "rotated q differs"
+    ka, va = layer_bits(w_a.manager, layer)
+    kb, vb = layer_bits(w_b.manager, layer)
+    assert np.array_equal(ka, kb), "K pool differs"
+    assert np.array_equal(va, vb), "V pool differs"
+    assert np.array_equal(bits(out_f), bits(out_s)), "attention differs"
+    return q_f, out_f
+
+
+@pytest.mark.parametrize("name", ["decode_b1", "decode_b32", "decode_32k"])
+def test_fused_decode_append_matches_two_calls_and_oracle(name):
+    say(f"[fused decode {name}]")
+    w_a = make_workload(name, device=DEV)
+    pre_k, pre_v = layer_bits(w_a.manager)
+    w_b = make_workload(name, device=DEV)
+    q_f, out_f = _fused_vs_two_calls(w_a, w_b)
+    post_k, post_v = layer_bits(w_a.manager)
+    pk, pv, q_exp, o_exp = oracle_step(w_a, pre_k, pre_v)
+    assert np.array_equal(bits(q_f), q_exp)
+    assert np.array_equal(post_k, pk) and np.array_equal(post_v, pv)
+    assert_attention_close(bits(out_f), o_exp, f"fused {name}")
+
+
+def test_fused_decode_append_ragged_and_many_short_sequences():
+    """Contexts around slice and page edges, and 100 one-to-three-token
+    contexts (chunks of many pieces, several new rows per chunk)."""
+    for cache_lens in ([0, 30, 31, 32, 127, 128, 129, 255, 256, 1000, 4095],
+                       [i % 3 for i in range(100)]):
+        say(f"[fused ragged {cache_lens[:6]}...]")
+        lengths = (cache_lens, [1] * len(cache_lens))
+        w_a = make_workload("decode_b32", device=DEV, lengths=lengths)
+        w_b = make_workload("decode_b32", device=DEV, lengths=lengths)
+        pre_k, pre_v = layer_bits(w_a.manager)
+        q_f, out_f = _fused_vs_two_calls(w_a, w_b)
+        _, _, q_exp, o_exp = oracle_step(w_a, pre_k, pre_v)
+        assert np.array_equal(bits(q_f), q_exp)
+        assert_attention_close(bits(out_f), o_exp, "fused ragged")
+
+
+def test_fused_decode_graph_replay_matches_eager():
+    say("[graph replay decode_layer]")
+    w = make_workload("decode_b32", device=DEV, num_layers=1)
+    batch = w.begin()
+    batch.plan(w.q.shape[1])
+
+    def step():
+        return batch.decode_layer(0, w.q, w.k, w.v, w.q_norm_w, w.k_norm_w, EPS, w.cos, w.sin)
+
+    q_e, out_e = step()
+    torch.cuda.synchronize()
+    q_e, out_e = bits(q_e), bits(out_e)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        q_g, out_g = step()
+    for rep in range(3):
+        q_g.zero_()
+        out_g.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(q_g), q_e), f"replay {rep}: rotated q differs"
+        assert np.array_equal(bits(out_g), out_e), f"replay {rep}: attention differs"
