@@ -367,3 +367,65 @@ def test_fused_decode_graph_replay_matches_eager():
         torch.cuda.synchronize()
         assert np.array_equal(bits(q_g), q_e), f"replay {rep}: rotated q differs"
         assert np.array_equal(bits(out_g), out_e), f"replay {rep}: attention differs"
+
+
+def _custom_workload(hq, hkv, cache_lens, q_lens, page_size=128, seed=5):
+    """A Workload of any head geometry (not the Qwen3-4B one): random pool,
+    pages placed by a seeded permutation, raw q/k/v, norm weights, rope."""
+    from hayate_amd.workloads import SPECS, Workload
+
+    d = 128
+    g = torch.Generator().manual_seed(seed)
+    need = [math.ceil((c + q) / page_size) for c, q in zip(cache_lens, q_lens)]
+    n_pages = sum(need) + 4
+    m = PagedKVCacheManager(1, hkv, d, n_pages * page_size, page_size, len(q_lens),
+                            torch.bfloat16, DEV, num_q_heads=hq)
+    m.k_cache.copy_(torch.randn(m.k_cache.shape, generator=g).to(torch.bfloat16))
+    m.v_cache.copy_(torch.randn(m.v_cache.shape, generator=g).to(torch.bfloat16))
+    perm = torch.randperm(m.num_pages, generator=g).tolist()
+    handles, cur = [], 0
+    for c, n in zip(cache_lens, need):
+        h = m.allocate()
+        m.claim_pages(h, perm[cur : cur + n])
+        cur += n
+        h.length = c
+        handles.append(h)
+    n_tok = sum(q_lens)
+    cos, sin = compute_rope_params(d, 1e6, max(c + q for c, q in zip(cache_lens, q_lens)) + 1,
+                                   device=DEV)
+    return Workload(
+        spec=SPECS["decode_b1"], manager=m, handles=handles, q_lens=list(q_lens),
+        cache_lens=list(cache_lens), page_lists=[list(h.pages) for h in handles],
+        q=torch.randn(n_tok, hq, d, generator=g).to(torch.bfloat16).to(DEV),
+        k=torch.randn(n_tok, hkv, d, generator=g).to(torch.bfloat16).to(DEV),
+        v=torch.randn(n_tok, hkv, d, generator=g).to(torch.bfloat16).to(DEV),
+        q_norm_w=(1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV),
+        k_norm_w=(1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV),
+        cos=cos, sin=sin,
+    )
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (64, 8), (64, 4)])
+def test_other_gqa_groups_mixed_and_fused_decode(hq, hkv):
+    """GQA groups 1, 2, 8 and 16: a mixed tick (two prefill chunks, three
+    decode tokens) through the append + attention calls, and a decode tick
+    through the fused call, against the oracle."""
+    say(f"[gqa hq={hq} hkv={hkv}]")
+    cache_lens, q_lens = [0, 300, 5, 700, 2000], [200, 130, 1, 1, 1]
+    w = _custom_workload(hq, hkv, cache_lens, q_lens)
+    pre_k, pre_v = layer_bits(w.manager)
+    q_rot, out = gpu_step(w)
+    post_k, post_v = layer_bits(w.manager)
+    pk, pv, q_exp, o_exp = oracle_step(w, pre_k, pre_v)
+    assert np.array_equal(bits(q_rot), q_exp)
+    assert np.array_equal(post_k, pk) and np.array_equal(post_v, pv)
+    assert_attention_close(bits(out), o_exp, f"mixed G={hq // hkv}")
+
+    cache_lens = [0, 31, 32, 129, 1000, 2047, 3, 64]
+    w_a = _custom_workload(hq, hkv, cache_lens, [1] * len(cache_lens), seed=6)
+    w_b = _custom_workload(hq, hkv, cache_lens, [1] * len(cache_lens), seed=6)
+    pre_k, pre_v = layer_bits(w_a.manager)
+    q_f, out_f = _fused_vs_two_calls(w_a, w_b)
+    _, _, q_exp, o_exp = oracle_step(w_a, pre_k, pre_v)
+    assert np.array_equal(bits(q_f), q_exp)
+    assert_attention_close(bits(out_f), o_exp, f"fused G={hq // hkv}")
