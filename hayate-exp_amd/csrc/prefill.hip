@@ -27,9 +27,11 @@
 //   O^T += V^T P^T  B = P^T: the first (last) eight of the lane's scores
 //                 are row c's probabilities for MFMA k index 8 h + j once k
 //                 stands for key 16 kh + (j < 4 ? 4 h + j : 8 + 4 h + j - 4);
-//                 A = V^T from LDS with ds_read_b64_tr_b16 (288-byte rows,
-//                 conflict-free), which hands lane r of a 16-lane group four
-//                 consecutive keys of dim r.
+//                 A = V^T from LDS with ds_read_b64_tr_b16, which hands lane
+//                 r of a 16-lane group four consecutive keys of dim r. One
+//                 read instruction serves 32 lanes (four rows x 64 bytes)
+//                 per LDS cycle; a 320-byte row pitch (80 dwords, 16 mod 64
+//                 banks) puts those four rows on disjoint banks.
 // K/V tiles of KEYS keys are double buffered in LDS: the next tile is loaded
 // into registers while the current one is computed, then stored, then one
 // barrier. The softmax rescales lazily: the exponent base of a row only
@@ -60,7 +62,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRows = kPrefillRows;  // (token, head) rows per workgroup
 constexpr int kThreads = 2 * kRows;  // one wave per 32 rows
 constexpr int kKRow = 136;     // u16 per K row in LDS (272 bytes)
-constexpr int kVRow = 144;     // u16 per V row in LDS (288 bytes)
+constexpr int kVRow = 160;     // u16 per V row in LDS (320 bytes)
 constexpr float kLazy = 8.0f;  // rescale threshold, exp2 domain
 constexpr int kTileKeys = kPrefillTileKeys;  // keys per LDS stage
 
