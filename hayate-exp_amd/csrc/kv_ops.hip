@@ -75,7 +75,8 @@ __device__ __forceinline__ int64_t phys_token(const int32_t *__restrict__ pt,
 
 // ---------------------------------------------------------------------------
 // Plain append: pool[h, phys(b, c_b + i)] = src[b, i, h]  (K and V).
-// Row index r in [0, 2 * total_tokens * Hkv): first all K rows, then V rows.
+// Grid (token blocks of 16, 2 Hkv): blockIdx.y < Hkv is K head blockIdx.y,
+// the rest V heads; one 16-lane group per token.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void kv_append_kernel(
     uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool,
@@ -89,14 +90,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
   __shared__ int32_t s_cl[kLdsSeqs];
   const SeqMeta meta = stage_seq_meta(s_qs, s_cl, q_start, cache_lens, num_seqs);
   const int lane = threadIdx.x & 15;
-  const int64_t rows_per_kind = static_cast<int64_t>(total_tokens) * num_kv_heads;
-  const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 4);
-  if (row >= 2 * rows_per_kind) return;
-  const bool is_v = row >= rows_per_kind;
-  const int64_t r = is_v ? row - rows_per_kind : row;
-  const int tok = static_cast<int>(r / num_kv_heads);
-  const int h = static_cast<int>(r % num_kv_heads);
+  const int tok = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
+  if (tok >= total_tokens) return;
+  const bool is_v = static_cast<int>(blockIdx.y) >= num_kv_heads;
+  const int h = is_v ? blockIdx.y - num_kv_heads : blockIdx.y;
   const TokPos tp = meta.locate(tok);
   const int b = tp.seq;
   const int pos = tp.pos;
@@ -110,7 +107,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 
 // ---------------------------------------------------------------------------
 // Fused q/k RMSNorm + RoPE + K/V append.
-// Row index r over [q rows | k rows | v rows], each kind token-major.
+// Grid (token blocks of 16, Hq + 2 Hkv): blockIdx.y selects the q head, k
+// head or v head (in that order); one 16-lane group per token.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
@@ -128,24 +126,11 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
   __shared__ int32_t s_cl[kLdsSeqs];
   const SeqMeta meta = stage_seq_meta(s_qs, s_cl, q_start, cache_lens, num_seqs);
   const int lane = threadIdx.x & 15;
-  const int64_t nq = static_cast<int64_t>(total_tokens) * num_q_heads;
-  const int64_t nk = static_cast<int64_t>(total_tokens) * num_kv_heads;
-  const int64_t row =
-      static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 4);
-  if (row >= nq + 2 * nk) return;
-
-  int kind;  // 0 = q, 1 = k, 2 = v
-  int64_t r;
-  int heads;
-  if (row < nq) {
-    kind = 0; r = row; heads = num_q_heads;
-  } else if (row < nq + nk) {
-    kind = 1; r = row - nq; heads = num_kv_heads;
-  } else {
-    kind = 2; r = row - nq - nk; heads = num_kv_heads;
-  }
-  const int tok = static_cast<int>(r / heads);
-  const int h = static_cast<int>(r % heads);
+  const int tok = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
+  if (tok >= total_tokens) return;
+  const int slot_y = blockIdx.y;
+  const int kind = slot_y < num_q_heads ? 0 : slot_y < num_q_heads + num_kv_heads ? 1 : 2;  // q, k, v
+  const int h = kind == 0 ? slot_y : kind == 1 ? slot_y - num_q_heads : slot_y - num_q_heads - num_kv_heads;
   const TokPos tp = meta.locate(tok);
   const int b = tp.seq;
   const int pos = tp.pos;
@@ -289,8 +274,9 @@ extern "C" int hy_kv_append(void *k_pool, void *v_pool,
   HY_REQUIRE(k_pool && v_pool && k && v && q_start && cache_lens && page_table,
              "hy_kv_append: null pointer argument");
   if (total_tokens == 0) return HY_OK;
-  const int64_t rows = 2LL * total_tokens * num_kv_heads;
-  hipLaunchKernelGGL(hy::kv_append_kernel, dim3(hy::grid_for_rows(rows)),
+  HY_REQUIRE(2 * num_kv_heads <= 65535, "num_kv_heads (%d) too large", num_kv_heads);
+  hipLaunchKernelGGL(hy::kv_append_kernel,
+                     dim3(hy::grid_for_rows(total_tokens), 2 * num_kv_heads),
                      dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<uint16_t *>(k_pool),
                      static_cast<uint16_t *>(v_pool), pool_head_stride,
@@ -329,9 +315,11 @@ extern "C" int hy_qknorm_rope_append(
   HY_REQUIRE(cos_table == nullptr || max_positions > 0,
              "max_positions must be positive when tables are given");
   if (total_tokens == 0) return HY_OK;
-  const int64_t rows = static_cast<int64_t>(total_tokens) * (num_q_heads + 2 * num_kv_heads);
+  HY_REQUIRE(num_q_heads + 2 * num_kv_heads <= 65535, "too many heads (%d q, %d kv)",
+             num_q_heads, num_kv_heads);
   hipLaunchKernelGGL(
-      hy::qknorm_rope_append_kernel, dim3(hy::grid_for_rows(rows)), dim3(256),
+      hy::qknorm_rope_append_kernel,
+      dim3(hy::grid_for_rows(total_tokens), num_q_heads + 2 * num_kv_heads), dim3(256),
       0, static_cast<hipStream_t>(stream), static_cast<const uint16_t *>(q),
       q_stride_seq, q_stride_tok, q_stride_head, static_cast<uint16_t *>(q_out),
       qo_stride_seq, qo_stride_tok, qo_stride_head,

@@ -34,11 +34,34 @@ __device__ __forceinline__ u32x4 pack8_rne(const float (&y)[8]) {
 // the reciprocal are taken in fp64 and rounded to fp32, which equals the
 // correctly rounded fp32 operation (53 >= 2 * 24 + 2 makes the double
 // rounding innocuous for both), independent of fp32 sqrt/div lowering.
+// Lane data movement within 16-lane rows by DPP row rotations (VALU, no
+// LDS round trip). A row holds a head row in full, so every lane a rotation
+// reads is active whenever the destination is.
+template <int N>
+__device__ __forceinline__ uint32_t row_ror(uint32_t x) {
+  static_assert(N >= 1 && N <= 15, "row_ror:1..15");
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x120 + N, 0xf, 0xf, false));
+}
+template <int N>
+__device__ __forceinline__ double row_ror_f64(double x) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(x));
+  const uint64_t lo = row_ror<N>(static_cast<uint32_t>(u));
+  const uint64_t hi = row_ror<N>(static_cast<uint32_t>(u >> 32));
+  return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
+}
+// Value of lane l ^ 8 of the row (a rotation by 8 of 16).
+__device__ __forceinline__ float row_xor8(float x) {
+  return __uint_as_float(row_ror<8>(__float_as_uint(x)));
+}
+// Sum over the 16 lanes of a row, in every lane: rotations by 8, 4, 2, 1.
+// The terms are exact squares of bf16 values and fp64 holds their sum
+// exactly, so the order does not matter.
 __device__ __forceinline__ double row16_sum_f64(double x) {
-  x += __shfl_xor(x, 8, 16);
-  x += __shfl_xor(x, 4, 16);
-  x += __shfl_xor(x, 2, 16);
-  x += __shfl_xor(x, 1, 16);
+  x += row_ror_f64<8>(x);
+  x += row_ror_f64<4>(x);
+  x += row_ror_f64<2>(x);
+  x += row_ror_f64<1>(x);
   return x;
 }
 
@@ -71,7 +94,7 @@ __device__ __forceinline__ void rope8(float (&x)[8],
                                       int lane) {
   float other[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) other[j] = __shfl_xor(x[j], 8, 16);
+  for (int j = 0; j < 8; ++j) other[j] = row_xor8(x[j]);
   const float sgn = lane < 8 ? -1.0f : 1.0f;
   const f32x4 c0 = *reinterpret_cast<const f32x4 *>(cos_row + lane * 8);
   const f32x4 c1 = *reinterpret_cast<const f32x4 *>(cos_row + lane * 8 + 4);
