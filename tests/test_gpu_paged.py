@@ -207,6 +207,27 @@ def test_page_size_256():
     _ragged([300, 0, 1000], [1, 70, 1], page_size=256)
 
 
+def test_more_sequences_than_the_staged_metadata():
+    """1,100 sequences: past the 1,024 the append kernels stage in LDS, so
+    they look sequences up in global memory; decode chunks hold many
+    pieces. Plain and fused decode, then a mixed tick with prefill chunks."""
+    n = 1100
+    cache_lens = [(7 * i) % 300 for i in range(n)]
+    _ragged(cache_lens, [1] * n, pool_tokens=(n + 4) * 384)
+    lengths = (cache_lens, [1] * n)
+    w_a = make_workload("decode_b32", device=DEV, lengths=lengths)
+    w_b = make_workload("decode_b32", device=DEV, lengths=lengths)
+    pre_k, pre_v = layer_bits(w_a.manager)
+    q_f, out_f = _fused_vs_two_calls(w_a, w_b)
+    _, _, q_exp, o_exp = oracle_step(w_a, pre_k, pre_v)
+    assert np.array_equal(bits(q_f), q_exp)
+    assert_attention_close(bits(out_f), o_exp, "fused 1100")
+    q_lens = [1] * n
+    for i in (3, 500, 1099):
+        q_lens[i] = 70
+    _ragged(cache_lens, q_lens, pool_tokens=(n + 4) * 384)
+
+
 def test_copy_on_write_keeps_shared_pages_intact():
     say("[copy on write]")
     hq, hkv, d = 32, 8, 128
