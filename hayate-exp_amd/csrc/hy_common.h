@@ -60,15 +60,18 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// fp32 -> bf16 round-to-nearest-even, NaN -> 0x7fc0 (the rule torch's
-// c10::BFloat16 conversion uses), written out so results are bit-exact.
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
+// fp32 -> bf16 round-to-nearest-even by gfx950's v_cvt_pk_bf16_f32. For
+// every non-NaN input (all 2^32 fp32 patterns compared on MI355X) the result
+// is the one torch's c10::BFloat16 conversion gives, subnormals and
+// infinities included; a NaN becomes a quiet NaN that keeps its sign
+// (torch: 0x7fc0 for both signs).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
-  return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+  const bf16x2_t h = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // 16-byte global load / store of 8 bf16 values.

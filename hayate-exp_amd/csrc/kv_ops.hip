@@ -107,10 +107,17 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 
 // ---------------------------------------------------------------------------
 // Fused q/k RMSNorm + RoPE + K/V append.
-// Grid (token blocks of 16, Hq + 2 Hkv): blockIdx.y selects the q head, k
-// head or v head (in that order); one 16-lane group per token.
+// Grid (token blocks of 16, head groups): blockIdx.y walks the groups of
+// `spb` (<= kMaxSlots) q heads, then those of k heads, then those of v
+// heads; one 16-lane group per token. The token's sequence, position,
+// page, the group's norm weights and the cos/sin row are looked up once
+// per block, and every head's row load is issued before any is processed,
+// so a block keeps spb row loads in flight instead of one dependent chain
+// per head row.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
+constexpr int kMaxSlots = 8;
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void qknorm_rope_append_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
     uint16_t *__restrict__ q_out, int64_t qo_ss, int64_t qo_st, int64_t qo_sh,
     const uint16_t *__restrict__ k, int64_t k_ss, int64_t k_st, int64_t k_sh,
@@ -121,44 +128,77 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     uint16_t *__restrict__ v_pool, int64_t pool_hs,
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ cache_lens,
     const int32_t *__restrict__ page_table, int64_t pt_stride, int num_seqs,
-    int total_tokens, int num_q_heads, int num_kv_heads, int page_size) {
+    int total_tokens, int num_q_heads, int num_kv_heads, int page_size, int spb) {
   __shared__ int32_t s_qs[kLdsSeqs + 1];
   __shared__ int32_t s_cl[kLdsSeqs];
   const SeqMeta meta = stage_seq_meta(s_qs, s_cl, q_start, cache_lens, num_seqs);
   const int lane = threadIdx.x & 15;
   const int tok = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
   if (tok >= total_tokens) return;
-  const int slot_y = blockIdx.y;
-  const int kind = slot_y < num_q_heads ? 0 : slot_y < num_q_heads + num_kv_heads ? 1 : 2;  // q, k, v
-  const int h = kind == 0 ? slot_y : kind == 1 ? slot_y - num_q_heads : slot_y - num_q_heads - num_kv_heads;
+  const int gq = (num_q_heads + spb - 1) / spb;
+  const int gk = (num_kv_heads + spb - 1) / spb;
+  const int gy = blockIdx.y;
+  const int kind = gy < gq ? 0 : gy < gq + gk ? 1 : 2;  // q, k, v heads
+  const int h0 = (kind == 0 ? gy : kind == 1 ? gy - gq : gy - gq - gk) * spb;
+  const int nh = min(spb, (kind == 0 ? num_q_heads : num_kv_heads) - h0);
   const TokPos tp = meta.locate(tok);
   const int b = tp.seq;
   const int pos = tp.pos;
 
+  // Source rows: base + head * src_sh.
+  const uint16_t *src;
+  int64_t src_sh;
+  if (kind == 0) {
+    src = q + b * q_ss + static_cast<int64_t>(tok) * q_st;
+    src_sh = q_sh;
+  } else if (kind == 1) {
+    src = k + b * k_ss + static_cast<int64_t>(tok) * k_st;
+    src_sh = k_sh;
+  } else {
+    src = v + b * v_ss + static_cast<int64_t>(tok) * v_st;
+    src_sh = v_sh;
+  }
+  src += lane * 8;
+  u32x4 raw[kMaxSlots];
+#pragma unroll
+  for (int j = 0; j < kMaxSlots; ++j)
+    if (j < nh) raw[j] = load16(src + (h0 + j) * src_sh);
+
+  const int64_t p = kind == 0 ? 0 : phys_token(page_table, pt_stride, b, pos, page_size);
   if (kind == 2) {
-    const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);
-    const uint16_t *src = v + b * v_ss + static_cast<int64_t>(tok) * v_st + h * v_sh;
-    store16(v_pool + h * pool_hs + p * kHeadDim + lane * 8, load16(src + lane * 8));
+    uint16_t *dst = v_pool + p * kHeadDim + lane * 8;
+#pragma unroll
+    for (int j = 0; j < kMaxSlots; ++j)
+      if (j < nh) store16(dst + (h0 + j) * pool_hs, raw[j]);
     return;
   }
 
-  const uint16_t *src = kind == 0
-      ? q + b * q_ss + static_cast<int64_t>(tok) * q_st + h * q_sh
-      : k + b * k_ss + static_cast<int64_t>(tok) * k_st + h * k_sh;
-  float x[8];
-  unpack8(load16(src + lane * 8), x);
+  // Destination rows: the rotated q output, or the K pool.
+  uint16_t *dst = kind == 0 ? q_out + b * qo_ss + static_cast<int64_t>(tok) * qo_st
+                            : k_pool + p * kHeadDim;
+  const int64_t dst_sh = kind == 0 ? qo_sh : pool_hs;
+  dst += lane * 8;
   const uint16_t *w = kind == 0 ? q_w : k_w;
-  if (w != nullptr) rms_norm8(x, w, lane, eps);
-  if (cos_t != nullptr) {
+  float wf[8];
+  if (w != nullptr) unpack8(load16(w + lane * 8), wf);
+  float cs[8], sn[8];
+  const bool rot = cos_t != nullptr;
+  if (rot) {
     const int64_t off = static_cast<int64_t>(pos) * kHeadDim;
-    rope8(x, cos_t + off, sin_t + off, lane);
+    load_row8(cos_t + off, lane, cs);
+    load_row8(sin_t + off, lane, sn);
+    const float sgn = lane < 8 ? -1.0f : 1.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sn[j] *= sgn;
   }
-  const u32x4 y = pack8_rne(x);
-  if (kind == 0) {
-    store16(q_out + b * qo_ss + static_cast<int64_t>(tok) * qo_st + h * qo_sh + lane * 8, y);
-  } else {
-    const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);
-    store16(k_pool + h * pool_hs + p * kHeadDim + lane * 8, y);
+#pragma unroll
+  for (int j = 0; j < kMaxSlots; ++j) {
+    if (j >= nh) break;
+    float x[8];
+    unpack8(raw[j], x);
+    if (w != nullptr) rms_norm8(x, wf, eps);
+    if (rot) rope8_signed(x, cs, sn);
+    store16(dst + (h0 + j) * dst_sh, pack8_rne(x));
   }
 }
 
@@ -317,9 +357,17 @@ extern "C" int hy_qknorm_rope_append(
   if (total_tokens == 0) return HY_OK;
   HY_REQUIRE(num_q_heads + 2 * num_kv_heads <= 65535, "too many heads (%d q, %d kv)",
              num_q_heads, num_kv_heads);
+  // Heads per block: as many as keep about four blocks per CU, so that
+  // short ticks still spread over the chip.
+  const int64_t token_blocks = hy::grid_for_rows(total_tokens);
+  auto groups = [&](int spb) {
+    return (num_q_heads + spb - 1) / spb + 2 * ((num_kv_heads + spb - 1) / spb);
+  };
+  int spb = hy::kMaxSlots;
+  while (spb > 1 && token_blocks * groups(spb) < 1024) spb /= 2;
   hipLaunchKernelGGL(
       hy::qknorm_rope_append_kernel,
-      dim3(hy::grid_for_rows(total_tokens), num_q_heads + 2 * num_kv_heads), dim3(256),
+      dim3(token_blocks, groups(spb)), dim3(256),
       0, static_cast<hipStream_t>(stream), static_cast<const uint16_t *>(q),
       q_stride_seq, q_stride_tok, q_stride_head, static_cast<uint16_t *>(q_out),
       qo_stride_seq, qo_stride_tok, qo_stride_head,
@@ -330,7 +378,7 @@ extern "C" int hy_qknorm_rope_append(
       static_cast<const uint16_t *>(k_norm_weight), eps, cos_table, sin_table,
       static_cast<uint16_t *>(k_pool), static_cast<uint16_t *>(v_pool),
       pool_head_stride, q_start, cache_lens, page_table, page_table_stride,
-      num_seqs, total_tokens, num_q_heads, num_kv_heads, page_size);
+      num_seqs, total_tokens, num_q_heads, num_kv_heads, page_size, spb);
   return hy::launch_status("hy_qknorm_rope_append");
 }
 

@@ -40,8 +40,7 @@ __device__ __forceinline__ u32x4 pack8_rne(const float (&y)[8]) {
 template <int N>
 __device__ __forceinline__ uint32_t row_ror(uint32_t x) {
   static_assert(N >= 1 && N <= 15, "row_ror:1..15");
-  return static_cast<uint32_t>(
-      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x120 + N, 0xf, 0xf, false));
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x120 + N, 0xf, 0xf, false));
 }
 template <int N>
 __device__ __forceinline__ double row_ror_f64(double x) {
@@ -65,9 +64,8 @@ __device__ __forceinline__ double row16_sum_f64(double x) {
   return x;
 }
 
-__device__ __forceinline__ void rms_norm8(float (&x)[8],
-                                          const uint16_t *__restrict__ w,
-                                          int lane, float eps) {
+// wf: the 8 weights of this lane's features, already widened to fp32.
+__device__ __forceinline__ void rms_norm8(float (&x)[8], const float (&wf)[8], float eps) {
   double ss = 0.0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ss += static_cast<double>(x[j] * x[j]);
@@ -75,39 +73,66 @@ __device__ __forceinline__ void rms_norm8(float (&x)[8],
   const float mean = static_cast<float>(ss) * (1.0f / kHeadDim);
   const float root = static_cast<float>(sqrt(static_cast<double>(mean + eps)));
   const float rstd = static_cast<float>(1.0 / static_cast<double>(root));
-  const u32x4 wv = load16(w + lane * 8);
-  float wf[8];
-  unpack8(wv, wf);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float y = (x[j] * rstd) * wf[j];
-    x[j] = bf16_to_f32(static_cast<uint16_t>(f32_to_bf16_rne(y)));
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = pack_bf16x2_rne((x[2 * j] * rstd) * wf[2 * j],
+                                       (x[2 * j + 1] * rstd) * wf[2 * j + 1]);
+    x[2 * j] = bf16_lo(w);
+    x[2 * j + 1] = bf16_hi(w);
   }
+}
+
+__device__ __forceinline__ void rms_norm8(float (&x)[8],
+                                          const uint16_t *__restrict__ w,
+                                          int lane, float eps) {
+  float wf[8];
+  unpack8(load16(w + lane * 8), wf);
+  rms_norm8(x, wf, eps);
 }
 
 // y = bf16(x * cos + rotate_half(x) * sin), rotate_half(x) = cat(-x2, x1)
 // (hayate/model/rope.py:31-47). Lane l holds features 8l..8l+7; its partner
 // l ^ 8 holds the other half.
+// c: cos of this lane's 8 features at the token's position; ss: their sin
+// times -1 in lanes 0-7 (the half that rotate_half negates) and +1 in lanes
+// 8-15. Negation is exact and (-o) * s rounds to o * (-s) bit for bit, so
+// folding the sign into the table is the reference's arithmetic.
+__device__ __forceinline__ void rope8_signed(float (&x)[8], const float (&c)[8],
+                                             const float (&ss)[8]) {
+  float other[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) other[j] = row_xor8(x[j]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float a = x[j] * c[j];
+    const float r = other[j] * ss[j];
+    x[j] = a + r;
+  }
+}
+
+// Loads this lane's 8 entries of a 128-wide fp32 table row.
+__device__ __forceinline__ void load_row8(const float *__restrict__ row, int lane,
+                                          float (&out)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4 *>(row + lane * 8);
+  const f32x4 b = *reinterpret_cast<const f32x4 *>(row + lane * 8 + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    out[j] = a[j];
+    out[4 + j] = b[j];
+  }
+}
+
 __device__ __forceinline__ void rope8(float (&x)[8],
                                       const float *__restrict__ cos_row,
                                       const float *__restrict__ sin_row,
                                       int lane) {
-  float other[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) other[j] = row_xor8(x[j]);
+  float c[8], s[8];
+  load_row8(cos_row, lane, c);
+  load_row8(sin_row, lane, s);
   const float sgn = lane < 8 ? -1.0f : 1.0f;
-  const f32x4 c0 = *reinterpret_cast<const f32x4 *>(cos_row + lane * 8);
-  const f32x4 c1 = *reinterpret_cast<const f32x4 *>(cos_row + lane * 8 + 4);
-  const f32x4 s0 = *reinterpret_cast<const f32x4 *>(sin_row + lane * 8);
-  const f32x4 s1 = *reinterpret_cast<const f32x4 *>(sin_row + lane * 8 + 4);
-  const float c[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-  const float s[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float a = x[j] * c[j];
-    const float r = (sgn * other[j]) * s[j];
-    x[j] = a + r;
-  }
+  for (int j = 0; j < 8; ++j) s[j] *= sgn;
+  rope8_signed(x, c, s);
 }
 
 }  // namespace hy
