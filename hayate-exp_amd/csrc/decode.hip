@@ -488,19 +488,24 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
 
 // Combines the partials of every decode sequence: grid (merge item, q head
 // group of 4), 128 threads = 4 heads x 32 lanes x 4 dims. Item = {seq,
-// first_slot, num_partials, 0}. Up to eight partials are loaded in one
-// round of independent loads.
+// first_slot, num_partials, q_row = q_start[seq]}. Up to eight partials are
+// loaded in one round of independent loads: every load reads a real
+// partial (the split index is clamped to the last one) and the ones past
+// num_partials are then replaced by the empty partial, so no load sits
+// behind a branch. A lane whose head is past num_q_heads computes on a
+// clamped head and does not store.
 __global__ __launch_bounds__(128) void decode_merge_kernel(
     uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ items,
     const float *__restrict__ ws_acc, const float *__restrict__ ws_ml, int num_q_heads) {
-  const int32_t *it = items + 4 * blockIdx.x;
-  const int seq = it[0];
-  const int first = it[1];
-  const int nsplit = it[2];
-  const int hq = 4 * blockIdx.y + (threadIdx.x >> 5);
+  const int4 it = *reinterpret_cast<const int4 *>(items + 4 * blockIdx.x);
+  const int seq = it.x;
+  const int first = it.y;
+  const int nsplit = it.z;
+  const int hq_lane = 4 * blockIdx.y + (threadIdx.x >> 5);
+  const int hq = min(hq_lane, num_q_heads - 1);
   const int d = (threadIdx.x & 31) * 4;
-  if (hq >= num_q_heads) return;
+  const int64_t qs = it.w;  // q_start[seq], carried by the item
   float mx = -INFINITY, lsum = 0.f;
   f32x4 a = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < nsplit; s0 += 8) {
@@ -508,12 +513,18 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(
     f32x4 x[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int64_t base = static_cast<int64_t>(first + s0 + j) * num_q_heads + hq;
+      const int64_t base = static_cast<int64_t>(first + min(s0 + j, nsplit - 1)) * num_q_heads + hq;
+      const float2 ml = *reinterpret_cast<const float2 *>(ws_ml + base * 2);
+      m[j] = ml.x;
+      l[j] = ml.y;
+      x[j] = *reinterpret_cast<const f32x4 *>(ws_acc + base * kHeadDim + d);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
       const bool live = s0 + j < nsplit;
-      m[j] = live ? ws_ml[base * 2] : -INFINITY;
-      l[j] = live ? ws_ml[base * 2 + 1] : 0.f;
-      x[j] = live ? *reinterpret_cast<const f32x4 *>(ws_acc + base * kHeadDim + d)
-                  : f32x4{0.f, 0.f, 0.f, 0.f};
+      m[j] = live ? m[j] : -INFINITY;
+      l[j] = live ? l[j] : 0.f;
+      x[j] = live ? x[j] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     float cmx = mx;
 #pragma unroll
@@ -529,7 +540,8 @@ __global__ __launch_bounds__(128) void decode_merge_kernel(
     }
     mx = cmx;
   }
-  uint16_t *dst = out + seq * o_ss + static_cast<int64_t>(q_start[seq]) * o_st + hq * o_sh + d;
+  if (hq_lane >= num_q_heads) return;
+  uint16_t *dst = out + seq * o_ss + qs * o_st + hq * o_sh + d;
   *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2_rne(a[0] / lsum, a[1] / lsum),
                                                pack_bf16x2_rne(a[2] / lsum, a[3] / lsum));
 }

@@ -192,7 +192,7 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
       mt[0] = b;
       mt[1] = kDecodeWaves * seq_first;
       mt[2] = kDecodeWaves * np;
-      mt[3] = 0;
+      mt[3] = q_begin[b];
     }
     if (static_cast<int32_t>(pieces.size()) > first)
       chunks.push_back({first, static_cast<int32_t>(pieces.size()), slices});
@@ -295,7 +295,8 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
       mt[2] = t.q1;
       mt[3] = n_pslots;
       mt[4] = static_cast<int32_t>(parts);
-      mt[5] = mt[6] = mt[7] = 0;
+      mt[5] = q_begin[t.seq];
+      mt[6] = mt[7] = 0;
       n_pslots += static_cast<int32_t>(parts);
     }
   }

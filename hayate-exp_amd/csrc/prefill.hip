@@ -388,58 +388,75 @@ void prefill_kernel(
 }
 
 // Combines the splits of a query tile: grid (kv head, merge item, kRows /
-// 16 row groups), 512 threads = 16 rows x 32 lanes x 4 dims.
-// Item = {seq, q_begin, q_end, first_slot, num_splits, 0, 0, 0}. Up to
-// eight splits are loaded in one round of independent loads.
+// 32 row groups), 512 threads = 32 rows x 16 lanes x 8 dims. Item = {seq,
+// q_begin, q_end, first_slot, num_splits, q_row = q_start[seq], 0, 0}. Up
+// to four splits are loaded in one round of independent loads: every load
+// reads a real split (the index is clamped to the last one; a partial holds
+// all kRows rows, so rows past q_end are in bounds too) and the ones past
+// num_splits are then replaced by the empty partial, so no load sits behind
+// a branch. Rows past q_end are computed and not stored.
 template <int G>
 __global__ __launch_bounds__(512) void prefill_merge_kernel(
     uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ items,
     const float *__restrict__ ws_acc, const float *__restrict__ ws_ml, int num_kv_heads) {
-  const int32_t *it = items + 8 * blockIdx.y;
+  const int4 it0 = *reinterpret_cast<const int4 *>(items + 8 * blockIdx.y);
+  const int4 it1 = *reinterpret_cast<const int4 *>(items + 8 * blockIdx.y + 4);
   const int kvh = blockIdx.x;
-  const int seq = it[0];
-  const int q_begin = it[1];
-  const int q_end = it[2];
-  const int first = it[3];
-  const int nsplit = it[4];
-  const int r = 16 * blockIdx.z + (threadIdx.x >> 5);
-  const int d = (threadIdx.x & 31) * 4;
+  const int seq = it0.x;
+  const int q_begin = it0.y;
+  const int q_end = it0.z;
+  const int first = it0.w;
+  const int nsplit = it1.x;
+  const int r = 32 * blockIdx.z + (threadIdx.x >> 4);
+  const int d = (threadIdx.x & 15) * 8;
   const int i = q_begin + r / G;
-  if (i >= q_end) return;
+  const int64_t qs = it1.y;  // q_start[seq], carried by the item
   float mx = -INFINITY, lsum = 0.f;
-  f32x4 a = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < nsplit; s0 += 8) {
-    float m[8], l[8];
-    f32x4 x[8];
+  f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < nsplit; s0 += 4) {
+    float m[4], l[4];
+    f32x4 x0[4], x1[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t pr = (static_cast<int64_t>(first + s0 + j) * num_kv_heads + kvh) * kRows + r;
+    for (int j = 0; j < 4; ++j) {
+      const int64_t pr =
+          (static_cast<int64_t>(first + min(s0 + j, nsplit - 1)) * num_kv_heads + kvh) * kRows + r;
+      const float2 ml = *reinterpret_cast<const float2 *>(ws_ml + pr * 2);
+      m[j] = ml.x;
+      l[j] = ml.y;
+      x0[j] = *reinterpret_cast<const f32x4 *>(ws_acc + pr * kHeadDim + d);
+      x1[j] = *reinterpret_cast<const f32x4 *>(ws_acc + pr * kHeadDim + d + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
       const bool live = s0 + j < nsplit;
-      m[j] = live ? ws_ml[pr * 2] : -INFINITY;
-      l[j] = live ? ws_ml[pr * 2 + 1] : 0.f;
-      x[j] = live ? *reinterpret_cast<const f32x4 *>(ws_acc + pr * kHeadDim + d)
-                  : f32x4{0.f, 0.f, 0.f, 0.f};
+      m[j] = live ? m[j] : -INFINITY;
+      l[j] = live ? l[j] : 0.f;
+      x0[j] = live ? x0[j] : f32x4{0.f, 0.f, 0.f, 0.f};
+      x1[j] = live ? x1[j] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     float cmx = mx;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) cmx = fmaxf(cmx, m[j]);
-    if (cmx == -INFINITY) continue;
+    for (int j = 0; j < 4; ++j) cmx = fmaxf(cmx, m[j]);
+    // All maxima -inf: both factors below are 0 and every term adds +0.
     const float f_old = mx == -INFINITY ? 0.f : exp2f(mx - cmx);
     lsum *= f_old;
-    a *= f_old;
+    a0 *= f_old;
+    a1 *= f_old;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < 4; ++j) {
       const float f = m[j] == -INFINITY ? 0.f : exp2f(m[j] - cmx);
       lsum += f * l[j];
-      a += f * x[j];
+      a0 += f * x0[j];
+      a1 += f * x1[j];
     }
     mx = cmx;
   }
-  const int64_t qs = q_start[seq];
+  if (i >= q_end) return;
   uint16_t *dst = out + seq * o_ss + (qs + i) * o_st + (kvh * G + r % G) * o_sh + d;
-  *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2_rne(a[0] / lsum, a[1] / lsum),
-                                               pack_bf16x2_rne(a[2] / lsum, a[3] / lsum));
+  *reinterpret_cast<u32x4 *>(dst) =
+      u32x4{pack_bf16x2_rne(a0[0] / lsum, a0[1] / lsum), pack_bf16x2_rne(a0[2] / lsum, a0[3] / lsum),
+            pack_bf16x2_rne(a1[0] / lsum, a1[1] / lsum), pack_bf16x2_rne(a1[2] / lsum, a1[3] / lsum)};
 }
 
 template <int G>
@@ -460,7 +477,7 @@ template <int G>
 void launch_prefill_merge(hipStream_t st, int num_kv_heads, int n_merge, uint16_t *out,
                           int64_t o_ss, int64_t o_st, int64_t o_sh, const int32_t *q_start,
                           const int32_t *merge_items, const float *ws_acc, const float *ws_ml) {
-  hipLaunchKernelGGL(prefill_merge_kernel<G>, dim3(num_kv_heads, n_merge, kRows / 16), dim3(512),
+  hipLaunchKernelGGL(prefill_merge_kernel<G>, dim3(num_kv_heads, n_merge, kRows / 32), dim3(512),
                      0, st, out, o_ss, o_st, o_sh, q_start, merge_items, ws_acc, ws_ml,
                      num_kv_heads);
 }

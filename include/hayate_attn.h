@@ -134,15 +134,15 @@ int hy_page_scatter(void *pool, int64_t pool_layer_stride,
  *                 (the prefix sum of q_lens), q_pos = kv_len - 1 the
  *                 position of its query token and ends = 1 for the piece
  *                 that holds that position;
- *   merge items   int32[n][4] = {seq, first_slot, num_partials, 0}, one per
- *                 decode sequence (all of its pieces' partials);
+ *   merge items   int32[n][4] = {seq, first_slot, num_partials, q_row}, one
+ *                 per decode sequence (all of its pieces' partials);
  *   prefill items (q_len > 1): int32[n][8] =
  *                 {seq, q_begin, q_end, kv_begin, kv_end, slot, 0, 0}:
  *                 query tiles of 256 / G tokens, each over one range of keys
  *                 (kv_begin a multiple of 64), most keys first; slot as for
  *                 decode items;
  *   prefill merge items int32[n][8] =
- *                 {seq, q_begin, q_end, first_slot, num_splits, 0, 0, 0}.
+ *                 {seq, q_begin, q_end, first_slot, num_splits, q_row, 0, 0}.
  * Decode uses one chunk per CU and kv head (num_cus / num_kv_heads chunks,
  * at least 256 tokens each); a chunk also ends after as many pieces as the
  * kernel's query table holds. Prefill split lengths are chosen by

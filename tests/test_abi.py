@@ -81,6 +81,7 @@ def test_plan_decode_covers_every_token_once(split):
         assert (rows[:, 1] % 32 == 0).all() and (rows[:, 2] > rows[:, 1]).all()
         m = merged[b]
         assert m[1] == W * idx[0] and m[2] == W * len(idx)
+        assert m[3] == b  # the sequence's query row (q_start[b], q_len 1)
     assert p.n_slots == W * len(pieces) == int(p.merge[:, 2].sum())
     tokens = [int((pieces[c[0]:c[1], 2] - pieces[c[0]:c[1], 1]).sum()) for c in chunks]
     if split:
@@ -137,6 +138,7 @@ def test_plan_prefill_tiles_cover_every_query_and_key_once():
             else:
                 m = merges[(s_, q0)]
                 assert m[2] == q1 and m[4] == len(parts)
+                assert m[5] == sum(q[:s_])  # q_start of the sequence
                 assert sorted(parts[:, 5]) == list(range(m[3], m[3] + len(parts)))
     assert p.n_prefill_slots == int((pre[:, 5] >= 0).sum())
     # the 8192-token tile must have been split to balance the tick
