@@ -450,3 +450,27 @@ def test_other_gqa_groups_mixed_and_fused_decode(hq, hkv):
     _, _, q_exp, o_exp = oracle_step(w_a, pre_k, pre_v)
     assert np.array_equal(bits(q_f), q_exp)
     assert_attention_close(bits(out_f), o_exp, f"fused G={hq // hkv}")
+
+
+def test_append_partial_head_groups():
+    """12 q heads and 6 kv heads over 4,092 tokens (256 blocks of 16, enough
+    for the append launch to take groups of 8 heads per block): the last q
+    group holds 4 heads and the k and v groups 6; rotated q and both pools
+    bit-exact against the oracle."""
+    say("[append hq=12 hkv=6, 4,092 tokens]")
+    cache_lens, q_lens = [0, 100, 4000, 33, 77, 5000], [2000, 1500, 500, 90, 1, 1]
+    w = _custom_workload(12, 6, cache_lens, q_lens, seed=11)
+    pre_k, pre_v = layer_bits(w.manager)
+    batch = w.begin()
+    q_rot = batch.norm_rope_write_layer(0, w.q, w.k, w.v, w.q_norm_w, w.k_norm_w, EPS,
+                                        w.cos, w.sin)
+    torch.cuda.synchronize()
+    post_k, post_v = layer_bits(w.manager)
+    pk, pv = pre_k.copy(), pre_v.copy()
+    q_exp = R.qknorm_rope_append(bits(w.q), bits(w.k), bits(w.v), bits(w.q_norm_w),
+                                 bits(w.k_norm_w), EPS, w.cos.cpu().numpy(),
+                                 w.sin.cpu().numpy(), pk, pv, w.page_lists, w.cache_lens,
+                                 w.q_lens, w.manager.page_size)
+    assert np.array_equal(bits(q_rot), q_exp), "rotated q differs"
+    assert np.array_equal(post_k, pk), "K pool differs"
+    assert np.array_equal(post_v, pv), "V pool differs"
