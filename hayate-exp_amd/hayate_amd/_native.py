@@ -148,10 +148,10 @@ class TickPlan:
         # tok_end, slot_base, slice_begin, q_row, 0, 0}
         self.decode = decode
         self.n_chunks = n_chunks
-        self.merge = merge                  # int32 (n, 4) {seq, first_slot, num_partials, 0}
+        self.merge = merge                  # int32 (n, 4) {seq, first_slot, num_partials, q_row}
         self.n_slots = n_slots
         self.prefill = prefill              # int32 (n, 8) {seq, q0, q1, kv0, kv1, slot, 0, 0}
-        self.prefill_merge = prefill_merge  # int32 (n, 8) {seq, q0, q1, first_slot, splits, ..}
+        self.prefill_merge = prefill_merge  # int32 (n, 8) {seq, q0, q1, first_slot, splits, q_row, ..}
         self.n_prefill_slots = n_prefill_slots
 
 
