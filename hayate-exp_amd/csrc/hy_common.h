@@ -56,9 +56,6 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) {
 __device__ __forceinline__ float bf16_hi(uint32_t w) {
   return __uint_as_float(w & 0xffff0000u);
 }
-__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
-  return __uint_as_float(static_cast<uint32_t>(h) << 16);
-}
 
 // fp32 -> bf16 round-to-nearest-even by gfx950's v_cvt_pk_bf16_f32. For
 // every non-NaN input (all 2^32 fp32 patterns compared on MI355X) the result

@@ -61,10 +61,6 @@ __device__ __forceinline__ SeqMeta stage_seq_meta(int32_t *s_qs, int32_t *s_cl,
   return {s_qs, s_cl, q_start, cache_lens, num_seqs, staged};
 }
 
-struct RowAddr {
-  int64_t seq, tok, head;
-};
-
 // Physical token index of logical position t of sequence b.
 __device__ __forceinline__ int64_t phys_token(const int32_t *__restrict__ pt,
                                               int64_t pt_stride, int b, int t,
