@@ -474,3 +474,24 @@ def test_append_partial_head_groups():
     assert np.array_equal(bits(q_rot), q_exp), "rotated q differs"
     assert np.array_equal(post_k, pk), "K pool differs"
     assert np.array_equal(post_v, pv), "V pool differs"
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_mixed_ticks(seed):
+    """Seeded random ticks (Qwen3-4B heads): 3-12 sequences, each a decode
+    token or a prefill chunk of 2-300 tokens over 0-2,500 cached tokens, so
+    the planner's decode cuts and prefill key splits land at arbitrary
+    positions; pools and rotated q bit-exact, attention within tolerance."""
+    rng = np.random.default_rng(1000 + seed)
+    n = int(rng.integers(3, 13))
+    q_lens = [1 if rng.random() < 0.5 else int(rng.integers(2, 301)) for _ in range(n)]
+    cache_lens = [int(rng.integers(0, 2501)) for _ in range(n)]
+    say(f"[random tick seed={seed} q={q_lens} cache={cache_lens}]")
+    w = _custom_workload(32, 8, cache_lens, q_lens, seed=seed)
+    pre_k, pre_v = layer_bits(w.manager)
+    q_rot, out = gpu_step(w)
+    post_k, post_v = layer_bits(w.manager)
+    pk, pv, q_exp, o_exp = oracle_step(w, pre_k, pre_v)
+    assert np.array_equal(bits(q_rot), q_exp), "rotated q differs"
+    assert np.array_equal(post_k, pk) and np.array_equal(post_v, pv), "pools differ"
+    assert_attention_close(bits(out), o_exp, f"random tick {seed}")
