@@ -159,18 +159,21 @@ void prefill_kernel(
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
-  // Exponent base of this lane's row, in exp2 units and bf16-exact; -inf
-  // until the row has seen a key. The QK^T chain subtracts it (as r_mma,
-  // 0 while unset) with one more MFMA: A = 1 in k index 0 (a constant), B =
-  // -r_mma in k index 0 of this row, so the scores come out shifted and the
-  // probabilities are plain exp2 of them.
+  // Exponent base of this lane's row, in exp2 units (fp32); -inf until the
+  // row has seen a key. The QK^T chain subtracts it (as r_mma, 0 while
+  // unset) with one more MFMA: A = 1 in k indices 0-2 (a constant), B = the
+  // three bf16 parts of -r_mma (hi + mid + lo hold its 24 bits exactly) in
+  // k indices 0-2 of this row, so the scores come out shifted by the exact
+  // base and the probabilities are plain exp2 of them. With an exact base
+  // the row max's probability is exactly 1 when the base is set, so its
+  // bf16 rounding for the P V product matches the fp32 row sum.
   float base = -INFINITY;
   float r_mma = 0.f;
   float l_run = 0.f;
   bf16x8 shift_a, shift_b;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    shift_a[e] = static_cast<__bf16>(e == 0 && h == 0 ? 1.0f : 0.0f);
+    shift_a[e] = static_cast<__bf16>(e < 3 && h == 0 ? 1.0f : 0.0f);
     shift_b[e] = static_cast<__bf16>(0.0f);
   }
 
@@ -260,10 +263,10 @@ void prefill_kernel(
     mx = halves_max(mx);  // row max relative to r_mma
     // The base only moves when the row max exceeds it by more than kLazy
     // (from -inf: at the first visible key), so probabilities stay below
-    // 2^kLazy; the new base is the row max rounded to bf16.
+    // 2^kLazy; the new base is the row max.
     const bool need = base == -INFINITY ? mx != -INFINITY : mx > kLazy;
     if (__builtin_expect(__any(need), 0)) {
-      const float r_new = need ? __uint_as_float(f32_to_bf16_rne(mx + r_mma) << 16) : r_mma;
+      const float r_new = need ? mx + r_mma : r_mma;
       const float delta = r_new - r_mma;
       const float alpha = base == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(-delta);
       if (need) {
@@ -275,7 +278,12 @@ void prefill_kernel(
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-      shift_b[0] = static_cast<__bf16>(h == 0 ? -r_mma : 0.0f);
+      const float hi = __uint_as_float(f32_to_bf16_rne(r_mma) << 16);
+      const float mid = __uint_as_float(f32_to_bf16_rne(r_mma - hi) << 16);
+      const float lo = r_mma - hi - mid;  // at most 8 significant bits left
+      shift_b[0] = static_cast<__bf16>(h == 0 ? -hi : 0.0f);
+      shift_b[1] = static_cast<__bf16>(h == 0 ? -mid : 0.0f);
+      shift_b[2] = static_cast<__bf16>(h == 0 ? -lo : 0.0f);
     }
     float psum = 0.f;
 #pragma unroll
