@@ -495,3 +495,42 @@ def test_random_mixed_ticks(seed):
     assert np.array_equal(bits(q_rot), q_exp), "rotated q differs"
     assert np.array_equal(post_k, pk) and np.array_equal(post_v, pv), "pools differ"
     assert_attention_close(bits(out), o_exp, f"random tick {seed}")
+
+
+def test_few_key_rows_exact_base():
+    """Rows that see 1-4 keys (the first tokens of a chunk at offset 0) put
+    most weight on one key, so an error in that key's probability shows in
+    the output. The prefill kernel subtracts the exact fp32 row max, so the
+    largest probability is exactly 1 in bf16 as in the fp32 row sum. On
+    these seeded inputs the rows' max-abs error is 0.0082 (a base rounded
+    to bf16 gave 0.0156); the bound sits between the two."""
+    say("[few-key rows, chunk at offset 0]")
+    g = torch.Generator().manual_seed(21)
+    m = PagedKVCacheManager(1, 8, 128, 8192, 128, 2, torch.bfloat16, DEV, num_q_heads=32)
+    m.k_cache.copy_(torch.randn(m.k_cache.shape, generator=g).to(torch.bfloat16))
+    m.v_cache.copy_(torch.randn(m.v_cache.shape, generator=g).to(torch.bfloat16))
+    handles = []
+    for c in (0, 130):
+        h = m.allocate()
+        m.reserve(h, c)
+        h.length = c
+        handles.append(h)
+    q_lens = [64, 40]
+    q = torch.randn(sum(q_lens), 32, 128, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(sum(q_lens), 8, 128, generator=g).to(torch.bfloat16).to(DEV)
+    v = torch.randn(sum(q_lens), 8, 128, generator=g).to(torch.bfloat16).to(DEV)
+    pre_k = R.torch_bf16_to_bits(m.k_cache[0, 0])
+    pre_v = R.torch_bf16_to_bits(m.v_cache[0, 0])
+    batch = m.begin_tick(handles, q_lens)
+    batch.write_layer(0, k, v)
+    out = batch.attend_layer(q, 0)
+    torch.cuda.synchronize()
+    pages = [list(h.pages) for h in handles]
+    R.kv_append(pre_k, pre_v, bits(k), bits(v), pages, [0, 130], q_lens, 128)
+    exp = R.paged_attention(bits(q), pre_k, pre_v, pages, [0, 130], q_lens, 128)
+    got = R.bf16_to_f32(bits(out)).astype(np.float64).reshape(exp.shape)
+    rows = slice(0, 4)  # tokens 0-3 of the first sequence: 1-4 keys
+    e = exp[rows]
+    err = np.abs(got[rows] - e)
+    say(f"  max_abs {err.max():.4f}")
+    assert err.max() <= 0.011, err.max()
