@@ -242,6 +242,7 @@ struct AppendArgs {
   const uint16_t *q_w, *k_w;
   float eps;
   const float *cos_t, *sin_t;
+  int max_pos;  // rows of cos_t / sin_t
   const int32_t *cache_lens;
 };
 
@@ -409,8 +410,11 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
       const int32_t *pr = pieces + 8 * (pb + j);
       const int seq = pr[0];
       const int pos = pr[6];  // position of the step's token (its cache length)
-      const float *cos_row = ap.cos_t ? ap.cos_t + static_cast<int64_t>(pos) * kHeadDim : nullptr;
-      const float *sin_row = ap.sin_t ? ap.sin_t + static_cast<int64_t>(pos) * kHeadDim : nullptr;
+      // pos < max_pos is the caller's contract; the clamp only keeps a call
+      // that breaks it inside the tables.
+      const int64_t trow = static_cast<int64_t>(min(pos, ap.max_pos - 1)) * kHeadDim;
+      const float *cos_row = ap.cos_t ? ap.cos_t + trow : nullptr;
+      const float *sin_row = ap.sin_t ? ap.sin_t + trow : nullptr;
       if (row < n_p * G) {
         const int hh = row % G;
         const int qt = pr[5];
@@ -597,6 +601,7 @@ int paged_decode_impl(const char *name, const void *q, int64_t q_stride_seq,
                        "page_size %d unsupported (power of two >= 32 required)", page_size);
   HY_REQUIRE(n_decode >= 0 && n_slots >= 0, "item counts must be non-negative");
   if (n_decode == 0) return HY_OK;
+  HY_REQUIRE(n_decode <= 65535, "%d decode chunks exceed the grid limit of 65535", n_decode);
   HY_REQUIRE(q && out && k_pool && v_pool && page_table && q_start && decode_items,
              "%s: null pointer argument", name);
   const int G = num_q_heads / num_kv_heads;
@@ -703,6 +708,7 @@ extern "C" int hy_paged_decode_append(
   ap.eps = eps;
   ap.cos_t = cos_table;
   ap.sin_t = sin_table;
+  ap.max_pos = max_positions;
   ap.cache_lens = cache_lens;
   return paged_decode_impl("hy_paged_decode_append", q, q_stride_seq, q_stride_tok,
                            q_stride_head, out, k_pool, v_pool, pool_head_stride, page_table,

@@ -124,7 +124,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void q
     uint16_t *__restrict__ v_pool, int64_t pool_hs,
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ cache_lens,
     const int32_t *__restrict__ page_table, int64_t pt_stride, int num_seqs,
-    int total_tokens, int num_q_heads, int num_kv_heads, int page_size, int spb) {
+    int total_tokens, int num_q_heads, int num_kv_heads, int page_size, int spb,
+    int max_positions) {
   __shared__ int32_t s_qs[kLdsSeqs + 1];
   __shared__ int32_t s_cl[kLdsSeqs];
   const SeqMeta meta = stage_seq_meta(s_qs, s_cl, q_start, cache_lens, num_seqs);
@@ -180,7 +181,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void q
   float cs[8], sn[8];
   const bool rot = cos_t != nullptr;
   if (rot) {
-    const int64_t off = static_cast<int64_t>(pos) * kHeadDim;
+    // Positions must be below max_positions (the caller's contract); the
+    // clamp only keeps a call that breaks it inside the tables.
+    const int64_t off = static_cast<int64_t>(min(pos, max_positions - 1)) * kHeadDim;
     load_row8(cos_t + off, lane, cs);
     load_row8(sin_t + off, lane, sn);
     const float sgn = lane < 8 ? -1.0f : 1.0f;
@@ -374,7 +377,7 @@ extern "C" int hy_qknorm_rope_append(
       static_cast<const uint16_t *>(k_norm_weight), eps, cos_table, sin_table,
       static_cast<uint16_t *>(k_pool), static_cast<uint16_t *>(v_pool),
       pool_head_stride, q_start, cache_lens, page_table, page_table_stride,
-      num_seqs, total_tokens, num_q_heads, num_kv_heads, page_size, spb);
+      num_seqs, total_tokens, num_q_heads, num_kv_heads, page_size, spb, max_positions);
   return hy::launch_status("hy_qknorm_rope_append");
 }
 

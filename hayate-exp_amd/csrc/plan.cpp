@@ -146,16 +146,25 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
   const int32_t max_pieces = hy::decode_max_pieces(G);
   int32_t n_merge = 0, n_pre = 0;
   {
-    int64_t pos = 0;        // stream position of the next token
-    int64_t chunk = 0;      // index of the chunk being filled
-    int32_t first = 0;      // its first piece
-    int32_t slices = 0;     // its slices so far
+    int64_t pos = 0;          // stream position of the next token
+    int64_t chunk = 0;        // index of the chunk being filled
+    int64_t chunk_start = 0;  // stream position where it began
+    int32_t first = 0;        // its first piece
+    int32_t slices = 0;       // its slices so far
     auto close_chunk = [&]() {
       if (static_cast<int32_t>(pieces.size()) > first)
         chunks.push_back({first, static_cast<int32_t>(pieces.size()), slices});
       first = static_cast<int32_t>(pieces.size());
       slices = 0;
       ++chunk;
+      chunk_start = pos;
+    };
+    // Where the chunk being filled should end: the rest of the stream shared
+    // evenly by the chunks still to fill. A chunk that the piece limit closed
+    // early thus leaves its unfilled share to all later chunks instead of
+    // moving every later cut one chunk ahead of the stream.
+    auto chunk_target = [&]() -> int64_t {
+      return chunk_start + (decode_tokens - chunk_start) / (n_chunks - chunk);
     };
     for (int b = 0; b < num_seqs; ++b) {
       if (q_lens[b] != 1) continue;
@@ -167,7 +176,7 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
         int64_t end = kv;
         bool cut = false;
         if (chunk < n_chunks - 1) {
-          const int64_t chunk_end = decode_tokens * (chunk + 1) / n_chunks;
+          const int64_t chunk_end = chunk_target();
           if (chunk_end - seq_pos < kv) {
             end = std::min<int64_t>(kv, std::max<int64_t>(t, (chunk_end - seq_pos + kSlice / 2) /
                                                                kSlice * kSlice));

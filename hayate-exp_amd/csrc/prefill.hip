@@ -527,6 +527,7 @@ extern "C" int hy_paged_prefill(
                        "page_size %d unsupported (power of two >= 32 required)", page_size);
   HY_REQUIRE(n_prefill >= 0 && n_slots >= 0, "item counts must be non-negative");
   if (n_prefill == 0) return HY_OK;
+  HY_REQUIRE(n_prefill <= 65535, "%d prefill items exceed the grid limit of 65535", n_prefill);
   HY_REQUIRE(q && out && k_pool && v_pool && page_table && q_start && kv_lens && prefill_items,
              "hy_paged_prefill: null pointer argument");
   const int64_t need = hy_prefill_workspace_bytes(n_slots, num_kv_heads, head_dim);
@@ -580,6 +581,7 @@ extern "C" int hy_paged_prefill_merge(void *out, int64_t o_stride_seq, int64_t o
   hy::clear_error();
   HY_REQUIRE(n_merge >= 0 && n_slots >= 0, "item counts must be non-negative");
   if (n_merge == 0) return HY_OK;
+  HY_REQUIRE(n_merge <= 65535, "%d merge items exceed the grid limit of 65535", n_merge);
   HY_REQUIRE(num_kv_heads >= 1 && num_q_heads >= num_kv_heads &&
                  num_q_heads % num_kv_heads == 0,
              "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",

@@ -781,7 +781,30 @@ class PagedKVCacheManager:
         if len({id(h) for h in handles}) != len(handles):
             raise ValueError("an attention batch cannot contain the same cache handle twice")
 
+    def _cow_pages_needed(self, handles: Sequence[PagedCacheHandle],
+                          q_lens: Sequence[int]) -> int:
+        """Pages that _make_private will copy for this batch: shared pages
+        (refcount > 1) that [length, length + q) of a handle touches,
+        counted in the order _make_private visits them (a copy drops the
+        original's count, so the last sharer in the batch writes in place)."""
+        refs: dict[int, int] = {}
+        copies = 0
+        for h, q in zip(handles, q_lens):
+            if q <= 0:
+                continue
+            first = h.length // self.page_size
+            last = (h.length + q - 1) // self.page_size
+            for idx in range(first, min(last + 1, len(h.pages))):
+                page = h.pages[idx]
+                r = refs.get(page, self._refs[page])
+                if r > 1:
+                    copies += 1
+                    refs[page] = r - 1
+        return copies
+
     def _reserve_all(self, handles: Sequence[PagedCacheHandle], q_lens: Sequence[int]) -> None:
+        """Reserve every handle's append space and copy the shared pages the
+        appends touch, or raise before changing anything."""
         kv_lengths = [h.length + q for h, q in zip(handles, q_lens)]
         additional = sum(
             max(0, math.ceil(kv / self.page_size) - len(h.pages))
@@ -792,9 +815,12 @@ class PagedKVCacheManager:
                 f"request needs more than the paged cache capacity of "
                 f"{self.capacity_tokens} tokens"
             )
-        if additional > len(self._free_pages):
+        copies = self._cow_pages_needed(handles, q_lens)
+        if copies:
+            _require_hip(self.k_cache, "copy-on-write of a shared page")
+        if additional + copies > len(self._free_pages):
             raise MemoryError(
-                f"paged KV cache is full: batch needs {additional} "
+                f"paged KV cache is full: batch needs {additional + copies} "
                 f"additional pages, but only {len(self._free_pages)} remain"
             )
         for h, kv in zip(handles, kv_lengths):
@@ -850,6 +876,10 @@ class PagedKVCacheManager:
         self.commit_tick(handles, [query_len] * len(handles))
 
     def commit_tick(self, handles: Sequence[PagedCacheHandle], query_lens: Sequence[int]) -> None:
+        """Advance each handle by its query length after a begin_tick batch
+        ran through every layer."""
+        if len(query_lens) != len(handles):
+            raise ValueError("one query length per handle is required")
         for handle, q in zip(handles, query_lens):
             if handle.released:
                 raise RuntimeError("cannot commit a released cache handle")

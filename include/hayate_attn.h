@@ -71,6 +71,9 @@ int hy_kv_append(void *k_pool, void *v_pool, int64_t pool_head_stride,
  * q' goes to q_out; k' and v (unchanged) are appended as hy_kv_append does.
  * q_norm_weight / k_norm_weight may be NULL (no norm); cos_table/sin_table
  * may be NULL (no rotation); tables are fp32 (max_positions, head_dim).
+ * Every position cache_lens[b] + i must be below max_positions: this is the
+ * caller's guarantee (the kernels clamp the table row so that a call which
+ * breaks it cannot read past the tables, but its rotation is then wrong).
  * Replaces GroupedQueryAttention.forward lines 62-75 (hayate/model/
  * attention.py:62-75: q_norm, k_norm, apply_rope_vectorized, write_layer),
  * with hayate/model/rope.py:31-47 for the rotation.
@@ -178,7 +181,8 @@ int64_t hy_decode_workspace_bytes(int32_t n_slots, int32_t num_q_heads,
  * writes the output rows (out and q_start are validated here but written
  * and read by the merge).
  * Causal semantics: the query of sequence b at position kv_len - 1 sees
- * every key k < kv_len (paged_cache.py:266-271).
+ * every key k < kv_len (paged_cache.py:266-271). n_decode is at most 65535
+ * (the grid's y limit); more returns HY_EINVAL.
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T == 1.
  */
 int hy_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
@@ -201,6 +205,8 @@ int hy_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
  * rotated q rows are written to q_out, the new K and V rows to their pages,
  * bit-identical to hy_qknorm_rope_append, and the attention partials to the
  * workspace as hy_paged_decode does (hy_paged_decode_merge then writes out).
+ * As for hy_qknorm_rope_append, cache_lens[b] < max_positions is the
+ * caller's guarantee.
  * One launch instead of two per decode layer: the workgroups rotate the
  * query rows of their pieces themselves and take the new token's K/V row
  * from LDS, so no workgroup waits for another's write.
@@ -254,7 +260,9 @@ int64_t hy_prefill_workspace_bytes(int32_t n_slots, int32_t num_kv_heads,
  * logical position cache_len_b + i sees every cached prefix key and the
  * chunk's keys up to itself. K/V are read through the page table. Split
  * query tiles leave fp32 partials in the workspace; hy_paged_prefill_merge,
- * enqueued after this call on the same stream, completes them.
+ * enqueued after this call on the same stream, completes them. n_prefill
+ * (and n_merge of the merge) is at most 65535 (the grid's y limit); more
+ * returns HY_EINVAL.
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T > 1.
  */
 int hy_paged_prefill(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,

@@ -10,9 +10,11 @@ default for attention, so the oracle is more accurate than any bf16 kernel).
 Each function cites the reference file:line it restates (paths relative to
 the reference repository root).
 
-Pinning (tests/test_oracle.py, tests/golden/): every function here is checked
-against a torch library routine, a brute-force loop or a closed form
-(see the test module docstring); none is "parity unpinned".
+Pinning (tests/test_oracle.py): every function here is checked against a
+torch library routine, the reference's own torch op chain, a brute-force
+loop or a closed form (see the test module docstring); none is "parity
+unpinned". The reference holds no golden vectors or fixtures for this path,
+so there is no tests/golden/ directory.
 """
 
 from __future__ import annotations

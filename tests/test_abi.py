@@ -103,6 +103,22 @@ def test_plan_chunk_holds_at_most_the_query_table():
     assert (chunks[1:, 0] == chunks[:-1, 1]).all()
 
 
+@pytest.mark.parametrize("seed", range(3))
+def test_plan_chunks_stay_balanced_when_the_piece_limit_closes_chunks(seed):
+    """G = 16 (32 q heads over 2 kv heads): the query table holds 8 pieces,
+    so 256 sequences close chunks early; the cuts after such a close follow
+    the stream position, so the largest chunk stays near the mean (cut
+    targets counted in closed chunks made it 1.34x)."""
+    rng = np.random.default_rng(seed)
+    kv = rng.integers(256, 4097, size=256)
+    p = plan([1] * 256, kv, hq=32, hkv=2)
+    chunks, pieces = chunks_and_pieces(p)
+    assert ((chunks[:, 1] - chunks[:, 0]) <= 8).all()
+    tokens = np.array([int((pieces[c[0]:c[1], 2] - pieces[c[0]:c[1], 1]).sum()) for c in chunks])
+    assert tokens.sum() == kv.sum()
+    assert tokens.max() <= 1.05 * tokens.mean()
+
+
 def test_plan_chunk_cut_rounds_to_32_tokens():
     p = plan([1], [300], split=256)
     chunks, pieces = chunks_and_pieces(p)

@@ -173,3 +173,71 @@ def test_copy_on_write_needs_a_device_pool():
     m.truncate(child, 200)  # the next append would land in a shared page
     with pytest.raises(RuntimeError):
         m.begin_batch([child], 1)
+
+
+def test_begin_batch_counts_copy_on_write_pages_before_changing_anything(monkeypatch):
+    """A batch whose appends need new pages and a copy of a shared page
+    either gets all of them or raises before any handle changes (the
+    reference's begin_batch checks its page need up front,
+    paged_cache.py:218-234). The copy itself is a device operation; the
+    device check is stubbed so the bookkeeping runs on a CPU pool."""
+    import hayate_amd.paged_cache as pc
+
+    monkeypatch.setattr(pc, "_require_hip", lambda t, what: None)
+    m = PagedKVCacheManager(1, 1, 128, 640, 128, 4, torch.bfloat16, "cpu")
+    parent = m.allocate()
+    m.reserve(parent, 256)
+    parent.length = 256
+    child = m.fork(parent, 256)
+    m.truncate(child, 200)  # its next append lands in the shared second page
+    a = m.allocate()
+    m.reserve(a, 128)
+    a.length = 128  # its next append needs a new page
+    spare = m.allocate()
+    m.reserve(spare, 1)
+    assert m.free_page_count == 1
+    before = (list(a.pages), list(child.pages), [m.page_refcount(p) for p in range(5)])
+    with pytest.raises(MemoryError):
+        m.begin_batch([a, child], 1)
+    assert (list(a.pages), list(child.pages), [m.page_refcount(p) for p in range(5)]) == before
+    assert m.free_page_count == 1
+    # with a second free page both the new page and the copy fit
+    m.release(spare)
+    shared = parent.pages[1]
+    m.begin_batch([a, child], 1)
+    assert len(a.pages) == 2 and child.pages[1] != shared
+    assert m.page_refcount(shared) == 1 and m.page_refcount(child.pages[1]) == 1
+    assert m.page_refcount(child.pages[0]) == 2
+    assert m.free_page_count == 0
+
+
+def test_copy_on_write_batch_with_two_sharers_copies_once(monkeypatch):
+    """Two handles sharing one page both append into it in one batch: the
+    first copies it, the last sharer then writes the original in place, so
+    the pre-check needs exactly one free page."""
+    import hayate_amd.paged_cache as pc
+
+    monkeypatch.setattr(pc, "_require_hip", lambda t, what: None)
+    m = PagedKVCacheManager(1, 1, 128, 384, 128, 3, torch.bfloat16, "cpu")
+    parent = m.allocate()
+    m.reserve(parent, 256)
+    parent.length = 256
+    child = m.fork(parent, 256)
+    m.truncate(parent, 200)
+    m.truncate(child, 150)
+    assert m.free_page_count == 1
+    m.begin_batch([parent, child], 1)
+    assert parent.pages[1] != child.pages[1]
+    assert m.free_page_count == 0
+    assert m.page_refcount(parent.pages[1]) == 1 and m.page_refcount(child.pages[1]) == 1
+    assert m.page_refcount(parent.pages[0]) == 2
+
+
+def test_commit_tick_needs_one_length_per_handle():
+    m = make_manager(max_requests=2)
+    a, b = m.allocate(), m.allocate()
+    m.reserve(a, 2)
+    m.reserve(b, 2)
+    with pytest.raises(ValueError):
+        m.commit_tick([a, b], [1])
+    assert a.length == 0 and b.length == 0

@@ -294,3 +294,98 @@ def test_attention_mutations_are_caught():
     # dropping the causal diagonal (one key fewer) must be visible
     out = R.paged_attention(q, pk, pv, pl, [299], [5], 128)
     assert R.compare(R.f32_to_bf16(out.astype(np.float32)), ref)["max_abs"] > 1e-3
+
+
+# ------------------------------------------------- fused norm + rope + append
+def _reference_chain(q, k, v, q_w, k_w, cos, sin, pool_k, pool_v, page_lists, cache_lens,
+                     page_size, rope_first=False, positions_from_zero=False):
+    """The reference's op chain for one paged layer on a uniform (B, T)
+    batch, written with the torch ops it uses:
+    nn.RMSNorm on (B, T, H, D) (attention.py:34-35, 62-63), transpose to
+    (B, H, T, D) (66-68), apply_rope_vectorized at position_ids =
+    arange(T) + cache_lens (rope.py:31-47, qwen.py:97-109), then
+    write_layer's indexing (paged_cache.py:49-60) for k and the un-normed v.
+    Mutations (for the sensitivity checks): rope_first rotates before the
+    norm; positions_from_zero drops cache_lens from the positions."""
+    B, T, _, D = q.shape
+    qn = torch.nn.RMSNorm(D, eps=1e-6, dtype=torch.bfloat16)
+    kn = torch.nn.RMSNorm(D, eps=1e-6, dtype=torch.bfloat16)
+    with torch.no_grad():
+        qn.weight.copy_(q_w)
+        kn.weight.copy_(k_w)
+    cl = torch.tensor(cache_lens, dtype=torch.long)
+    position_ids = torch.arange(T, dtype=torch.long).unsqueeze(0)
+    if not positions_from_zero:
+        position_ids = position_ids + cl.view(-1, 1)
+
+    def rope(x):  # x (B, H, T, D)
+        x1, x2 = x[..., : D // 2], x[..., D // 2 :]
+        rotated = torch.cat((-x2, x1), dim=-1)
+        out = (x * cos[position_ids].unsqueeze(1)) + (rotated * sin[position_ids].unsqueeze(1))
+        return out.to(dtype=x.dtype)
+
+    with torch.no_grad():
+        if rope_first:
+            q = rope(q.transpose(1, 2)).transpose(1, 2)
+            k = rope(k.transpose(1, 2)).transpose(1, 2)
+            q, k = qn(q), kn(k)
+            q, k = q.transpose(1, 2), k.transpose(1, 2)
+        else:
+            q, k = qn(q), kn(k)
+            q, k = rope(q.transpose(1, 2)), rope(k.transpose(1, 2))
+        v = v.transpose(1, 2)
+        # page table (B, num_pages), -1 padded (paged_cache.py:238-250)
+        width = max(len(pl) for pl in page_lists)
+        table = torch.full((B, width), -1, dtype=torch.long)
+        for row, pl in enumerate(page_lists):
+            table[row, : len(pl)] = torch.tensor(pl, dtype=torch.long)
+        logical = cl[:, None] + torch.arange(T, dtype=torch.long).view(1, -1)
+        phys = torch.gather(table, 1, logical // page_size) * page_size + logical % page_size
+        pool_k[:, phys, :] = k.permute(1, 0, 2, 3)
+        pool_v[:, phys, :] = v.permute(1, 0, 2, 3)
+    return q  # (B, Hq, T, D)
+
+
+def test_qknorm_rope_append_matches_reference_op_chain():
+    """qknorm_rope_append (the oracle of the fused append kernels) against
+    the reference's own op chain on a uniform batch with non-zero, unaligned
+    cache lengths: rotated q, K pool and V pool bit for bit. Two plausible
+    mistakes — rope before the norm, positions without cache_lens — change
+    the result, so the check would catch them in the oracle."""
+    B, T, Hq, Hkv, D, P = 3, 6, 4, 2, 128, 8
+    cache_lens = [0, 77, 130]
+    page_lists = [[11, 3], [20, 7, 14, 1, 9, 30, 25, 4, 12, 17, 2], [5, 8, 16, 0, 29, 31, 6, 10,
+                                                                     13, 15, 18, 19, 21, 22,
+                                                                     23, 24, 26, 27]]
+    g = torch.Generator().manual_seed(41)
+    q = (torch.randn(B, T, Hq, D, generator=g) * 2).to(torch.bfloat16)
+    k = (torch.randn(B, T, Hkv, D, generator=g) * 2).to(torch.bfloat16)
+    v = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16)
+    q_w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    k_w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    cos_np, sin_np = R.rope_tables(D, 1_000_000, 4096)
+    cos, sin = torch.from_numpy(cos_np), torch.from_numpy(sin_np)
+    cap = 32 * P
+    pool0_k = torch.randn(Hkv, cap, D, generator=g).to(torch.bfloat16)
+    pool0_v = torch.randn(Hkv, cap, D, generator=g).to(torch.bfloat16)
+
+    tk, tv = pool0_k.clone(), pool0_v.clone()
+    q_ref = _reference_chain(q, k, v, q_w, k_w, cos, sin, tk, tv, page_lists, cache_lens, P)
+
+    ok_k, ok_v = R.torch_bf16_to_bits(pool0_k).copy(), R.torch_bf16_to_bits(pool0_v).copy()
+    q_ours = R.qknorm_rope_append(
+        R.torch_bf16_to_bits(q.reshape(B * T, Hq, D)), R.torch_bf16_to_bits(k.reshape(B * T, Hkv, D)),
+        R.torch_bf16_to_bits(v.reshape(B * T, Hkv, D)), R.torch_bf16_to_bits(q_w),
+        R.torch_bf16_to_bits(k_w), 1e-6, cos_np, sin_np, ok_k, ok_v, page_lists, cache_lens,
+        [T] * B, P)
+    assert np.array_equal(q_ours, R.torch_bf16_to_bits(q_ref.transpose(1, 2).reshape(B * T, Hq, D)))
+    assert np.array_equal(ok_k, R.torch_bf16_to_bits(tk)), "K pool"
+    assert np.array_equal(ok_v, R.torch_bf16_to_bits(tv)), "V pool (v is appended un-normed)"
+
+    for mutation in ({"rope_first": True}, {"positions_from_zero": True}):
+        mk, mv = pool0_k.clone(), pool0_v.clone()
+        q_mut = _reference_chain(q, k, v, q_w, k_w, cos, sin, mk, mv, page_lists, cache_lens, P,
+                                 **mutation)
+        assert not np.array_equal(
+            q_ours, R.torch_bf16_to_bits(q_mut.transpose(1, 2).reshape(B * T, Hq, D))), mutation
+        assert not np.array_equal(ok_k, R.torch_bf16_to_bits(mk)), mutation
