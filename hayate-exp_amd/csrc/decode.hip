@@ -45,6 +45,8 @@
 // past the end of a context may hold any bits; their scores are masked and
 // their V values zeroed before the MFMA so that 0 * NaN never occurs.
 
+#include <mutex>
+
 #include "decode_shape.h"
 #include "hy_common.h"
 #include "qknorm.h"
@@ -672,25 +674,22 @@ extern "C" int hy_paged_decode(
                            stream, nullptr);
 }
 
-extern "C" int hy_paged_decode_append(
-    const void *q, int64_t q_stride_seq, int64_t q_stride_tok, int64_t q_stride_head,
-    void *q_out, int64_t qo_stride_seq, int64_t qo_stride_tok, int64_t qo_stride_head,
-    const void *k, int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
-    const void *v, int64_t v_stride_seq, int64_t v_stride_tok, int64_t v_stride_head,
-    const void *q_norm_weight, const void *k_norm_weight, float eps, const float *cos_table,
-    const float *sin_table, int32_t max_positions, void *out, void *k_pool, void *v_pool,
-    int64_t pool_head_stride, const int32_t *page_table, int64_t page_table_stride,
-    const int32_t *q_start, const int32_t *cache_lens, const int32_t *decode_items,
-    int32_t n_decode, int32_t n_slots, void *workspace, int64_t workspace_bytes,
-    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-    int32_t page_size, float scale, void *stream) {
-  hy::clear_error();
-  HY_REQUIRE(q_out && k && v && cache_lens, "hy_paged_decode_append: null pointer argument");
+namespace {
+
+// Validates and packs the fused append's inputs (shared by
+// hy_paged_decode_append and hy_paged_decode_append_noalloc).
+int fill_append_args(const char *name, hy::AppendArgs &ap, void *q_out, int64_t qo_stride_seq,
+                     int64_t qo_stride_tok, int64_t qo_stride_head, const void *k,
+                     int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
+                     const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
+                     int64_t v_stride_head, const void *q_norm_weight,
+                     const void *k_norm_weight, float eps, const float *cos_table,
+                     const float *sin_table, int32_t max_positions, const int32_t *cache_lens) {
+  HY_REQUIRE(q_out && k && v && cache_lens, "%s: null pointer argument", name);
   HY_REQUIRE((cos_table == nullptr) == (sin_table == nullptr),
              "cos_table and sin_table must both be given or both be NULL");
   HY_REQUIRE(cos_table == nullptr || max_positions > 0,
              "max_positions must be positive when tables are given");
-  hy::AppendArgs ap;
   ap.q_out = static_cast<uint16_t *>(q_out);
   ap.qo_ss = qo_stride_seq;
   ap.qo_st = qo_stride_tok;
@@ -710,26 +709,24 @@ extern "C" int hy_paged_decode_append(
   ap.sin_t = sin_table;
   ap.max_pos = max_positions;
   ap.cache_lens = cache_lens;
-  return paged_decode_impl("hy_paged_decode_append", q, q_stride_seq, q_stride_tok,
-                           q_stride_head, out, k_pool, v_pool, pool_head_stride, page_table,
-                           page_table_stride, q_start, decode_items, n_decode, n_slots,
-                           workspace, workspace_bytes, num_seqs, num_q_heads, num_kv_heads,
-                           head_dim, page_size, scale, stream, &ap);
+  return HY_OK;
 }
 
-extern "C" int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,
-                                     int64_t o_stride_head, const int32_t *q_start,
-                                     const int32_t *merge_items, int32_t n_merge,
-                                     int32_t n_slots, const void *workspace,
-                                     int64_t workspace_bytes, int32_t num_q_heads,
-                                     int32_t head_dim, void *stream) {
-  hy::clear_error();
+// Validates and launches decode_merge_kernel over a workspace of n_slots
+// partials (shared by hy_paged_decode_merge and
+// hy_paged_decode_append_noalloc).
+int decode_merge_impl(const char *name, void *out, int64_t o_stride_seq, int64_t o_stride_tok,
+                      int64_t o_stride_head, const int32_t *q_start, const int32_t *merge_items,
+                      int32_t n_merge, int32_t n_slots, const void *workspace,
+                      int64_t workspace_bytes, int32_t num_q_heads, int32_t head_dim,
+                      void *stream) {
   HY_REQUIRE(n_merge >= 0 && n_slots >= 0, "item counts must be non-negative");
   if (n_merge == 0) return HY_OK;
   HY_REQUIRE_SUPPORTED(head_dim == kHeadDim, "head_dim %d unsupported (need %d)", head_dim,
                        kHeadDim);
-  HY_REQUIRE(out && q_start && merge_items && workspace,
-             "hy_paged_decode_merge: null pointer argument");
+  HY_REQUIRE(num_q_heads >= 1 && (num_q_heads + 3) / 4 <= 65535, "num_q_heads %d out of range",
+             num_q_heads);
+  HY_REQUIRE(out && q_start && merge_items && workspace, "%s: null pointer argument", name);
   const int64_t need = hy_decode_workspace_bytes(n_slots, num_q_heads, head_dim);
   if (workspace_bytes < need) {
     hy::set_error("workspace too small: need %lld bytes, got %lld",
@@ -744,5 +741,138 @@ extern "C" int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_
                      static_cast<hipStream_t>(stream), static_cast<uint16_t *>(out),
                      o_stride_seq, o_stride_tok, o_stride_head, q_start, merge_items, ws_acc,
                      ws_ml, num_q_heads);
-  return hy::launch_status("hy_paged_decode_merge");
+  return hy::launch_status(name);
+}
+
+}  // namespace
+
+extern "C" int hy_paged_decode_append(
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok, int64_t q_stride_head,
+    void *q_out, int64_t qo_stride_seq, int64_t qo_stride_tok, int64_t qo_stride_head,
+    const void *k, int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
+    const void *v, int64_t v_stride_seq, int64_t v_stride_tok, int64_t v_stride_head,
+    const void *q_norm_weight, const void *k_norm_weight, float eps, const float *cos_table,
+    const float *sin_table, int32_t max_positions, void *out, void *k_pool, void *v_pool,
+    int64_t pool_head_stride, const int32_t *page_table, int64_t page_table_stride,
+    const int32_t *q_start, const int32_t *cache_lens, const int32_t *decode_items,
+    int32_t n_decode, int32_t n_slots, void *workspace, int64_t workspace_bytes,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t page_size, float scale, void *stream) {
+  hy::clear_error();
+  hy::AppendArgs ap;
+  if (int rc = fill_append_args("hy_paged_decode_append", ap, q_out, qo_stride_seq,
+                                qo_stride_tok, qo_stride_head, k, k_stride_seq, k_stride_tok,
+                                k_stride_head, v, v_stride_seq, v_stride_tok, v_stride_head,
+                                q_norm_weight, k_norm_weight, eps, cos_table, sin_table,
+                                max_positions, cache_lens))
+    return rc;
+  return paged_decode_impl("hy_paged_decode_append", q, q_stride_seq, q_stride_tok,
+                           q_stride_head, out, k_pool, v_pool, pool_head_stride, page_table,
+                           page_table_stride, q_start, decode_items, n_decode, n_slots,
+                           workspace, workspace_bytes, num_seqs, num_q_heads, num_kv_heads,
+                           head_dim, page_size, scale, stream, &ap);
+}
+
+extern "C" int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,
+                                     int64_t o_stride_head, const int32_t *q_start,
+                                     const int32_t *merge_items, int32_t n_merge,
+                                     int32_t n_slots, const void *workspace,
+                                     int64_t workspace_bytes, int32_t num_q_heads,
+                                     int32_t head_dim, void *stream) {
+  hy::clear_error();
+  return decode_merge_impl("hy_paged_decode_merge", out, o_stride_seq, o_stride_tok,
+                           o_stride_head, q_start, merge_items, n_merge, n_slots, workspace,
+                           workspace_bytes, num_q_heads, head_dim, stream);
+}
+
+// ---------------------------------------------------------------------------
+// hy_paged_decode_append_noalloc: the fused decode step (decode kernel +
+// merge) with its fp32 partials in a file-scope device array instead of a
+// caller workspace, for callers that cannot allocate device memory.
+//
+// The array is HY_NOALLOC_SCRATCH_BYTES (8 MiB) per GPU, held for the life of
+// the process. Host code never passes the array's name to a kernel (on the
+// host it is a stand-in, not a device address): the first call on each
+// device, with that device current, resolves its address with
+// hipGetSymbolAddress and keeps it per device. Every call on one GPU shares
+// its array, so calls that overlap on one GPU (two streams, two threads)
+// race. Nothing in it needs clearing: the decode kernel writes every slot the
+// merge reads (each wave flushes a partial for every piece of its chunk,
+// empty ones included) before the merge, on the same stream, reads it.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[HY_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, or nullptr (the error
+// message is set).
+void *scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    hy::set_error("hy_paged_decode_append_noalloc: no usable current HIP device (%d)", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      hy::set_error("hy_paged_decode_append_noalloc: hipGetSymbolAddress failed on device %d: %s",
+                    dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int hy_paged_decode_append_noalloc(
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok, int64_t q_stride_head,
+    void *q_out, int64_t qo_stride_seq, int64_t qo_stride_tok, int64_t qo_stride_head,
+    const void *k, int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
+    const void *v, int64_t v_stride_seq, int64_t v_stride_tok, int64_t v_stride_head,
+    const void *q_norm_weight, const void *k_norm_weight, float eps, const float *cos_table,
+    const float *sin_table, int32_t max_positions, void *out, int64_t o_stride_seq,
+    int64_t o_stride_tok, int64_t o_stride_head, void *k_pool, void *v_pool,
+    int64_t pool_head_stride, const int32_t *page_table, int64_t page_table_stride,
+    const int32_t *q_start, const int32_t *cache_lens, const int32_t *decode_items,
+    int32_t n_decode, const int32_t *merge_items, int32_t n_merge, int32_t n_slots,
+    int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t page_size, float scale, void *stream) {
+  hy::clear_error();
+  HY_REQUIRE(n_slots >= 0 && num_q_heads >= 1, "item counts must be non-negative");
+  const int64_t need = hy_decode_workspace_bytes(n_slots, num_q_heads, head_dim);
+  if (need > HY_NOALLOC_SCRATCH_BYTES) {
+    hy::set_error("hy_paged_decode_append_noalloc: %d partial slots x %d heads need %lld bytes, "
+                  "more than the %lld-byte static scratch; use hy_paged_decode_append with a "
+                  "caller workspace",
+                  n_slots, num_q_heads, static_cast<long long>(need),
+                  static_cast<long long>(HY_NOALLOC_SCRATCH_BYTES));
+    return HY_ENOSPACE;
+  }
+  hy::AppendArgs ap;
+  if (int rc = fill_append_args("hy_paged_decode_append_noalloc", ap, q_out, qo_stride_seq,
+                                qo_stride_tok, qo_stride_head, k, k_stride_seq, k_stride_tok,
+                                k_stride_head, v, v_stride_seq, v_stride_tok, v_stride_head,
+                                q_norm_weight, k_norm_weight, eps, cos_table, sin_table,
+                                max_positions, cache_lens))
+    return rc;
+  if (n_decode == 0 && n_merge == 0) return HY_OK;
+  void *ws = scratch_on_current_device();
+  if (ws == nullptr) return HY_ELAUNCH;
+  if (int rc = paged_decode_impl("hy_paged_decode_append_noalloc", q, q_stride_seq, q_stride_tok,
+                                 q_stride_head, out, k_pool, v_pool, pool_head_stride,
+                                 page_table, page_table_stride, q_start, decode_items, n_decode,
+                                 n_slots, ws, HY_NOALLOC_SCRATCH_BYTES, num_seqs, num_q_heads,
+                                 num_kv_heads, head_dim, page_size, scale, stream, &ap))
+    return rc;
+  return decode_merge_impl("hy_paged_decode_append_noalloc", out, o_stride_seq, o_stride_tok,
+                           o_stride_head, q_start, merge_items, n_merge, n_slots, ws,
+                           HY_NOALLOC_SCRATCH_BYTES, num_q_heads, head_dim, stream);
 }

@@ -24,6 +24,8 @@ HY_EINVAL = -1
 HY_ELAUNCH = -2
 HY_EUNSUPPORTED = -3
 HY_ENOSPACE = -4
+# Static device scratch of hy_paged_decode_append_noalloc (bytes per GPU).
+NOALLOC_SCRATCH_BYTES = 8 * 1024 * 1024
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -73,6 +75,12 @@ _SIGNATURES = {
     ),
     "hy_paged_decode_merge": (
         [_P, _I64, _I64, _I64, _P, _P, _I32, _I32, _P, _I64, _I32, _I32, _P],
+        ctypes.c_int,
+    ),
+    "hy_paged_decode_append_noalloc": (
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64,
+         _I64, _P, _P, _F32, _P, _P, _I32, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P,
+         _P, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P],
         ctypes.c_int,
     ),
     "hy_prefill_tile_rows": ([], ctypes.c_int32),

@@ -383,13 +383,19 @@ class PagedKVBatch:
         cos: Optional[torch.Tensor],
         sin: Optional[torch.Tensor],
         scale: Optional[float] = None,
+        no_alloc: bool = False,
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """norm_rope_write_layer then attend_layer, for a batch whose
         sequences all decode one token, in one kernel launch plus the merge
         (attention.py:62-75 then paged_cache.py:62-71). Inputs as for
         norm_rope_write_layer; returns (q_rot, out) exactly as the two calls
         would: q_rot in the input layout, out as attend_layer returns it.
-        Pool contents and q_rot are bit-identical to the two-call path."""
+        Pool contents and q_rot are bit-identical to the two-call path.
+
+        no_alloc=True runs both launches through
+        hy_paged_decode_append_noalloc, whose partials live in the library's
+        static device scratch instead of the plan's workspace (same
+        results; raises MemoryError if the tick's partials do not fit)."""
         if any(ql != 1 for ql in self.q_lens):
             raise ValueError("decode_layer needs q_len == 1 for every sequence")
         a = self._append_inputs("decode_layer", q, k, v, q_norm_weight, k_norm_weight, cos,
@@ -414,6 +420,15 @@ class PagedKVBatch:
         k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
         stream = _stream_handle(self.device)
         lib = _native.lib()
+        if no_alloc:
+            self._launch("hy_paged_decode_append_noalloc", lib.hy_paged_decode_append_noalloc,
+                *a.head, float(eps), *a.tables, result.data_ptr(), *os_, k_ptr, v_ptr, hs,
+                self._pt_ptr, self._pt_stride, self._q_start_ptr, self._cache_lens_ptr,
+                plan.decode_ptr, plan.n_decode, plan.merge_ptr, plan.n_merge, plan.n_slots,
+                self.num_seqs, num_q_heads, self.num_kv_heads, self.head_dim, self.page_size,
+                float(scale), stream,
+            )
+            return a.q_out, result
         self._launch("hy_paged_decode_append", lib.hy_paged_decode_append,
             *a.head, float(eps), *a.tables, result.data_ptr(), k_ptr, v_ptr, hs,
             self._pt_ptr, self._pt_stride, self._q_start_ptr, self._cache_lens_ptr,

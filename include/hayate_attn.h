@@ -241,6 +241,43 @@ int hy_paged_decode_merge(void *out, int64_t o_stride_seq, int64_t o_stride_tok,
                           int64_t workspace_bytes, int32_t num_q_heads,
                           int32_t head_dim, void *stream);
 
+/* Size of the static device scratch of hy_paged_decode_append_noalloc, per
+ * GPU (8 MiB: the partials of 252 pieces at 32 query heads; the batch-32
+ * decode step needs about 2 MB). */
+#define HY_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
+
+/*
+ * hy_paged_decode_append followed by hy_paged_decode_merge, with the split
+ * partials in a static device array of HY_NOALLOC_SCRATCH_BYTES owned by the
+ * library instead of a caller workspace: a call allocates nothing (no
+ * hipMalloc, no allocating library routine). No counterpart in the
+ * reference: it is for callers that cannot allocate device memory — code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation. Arguments are those of the two calls it combines (out strides
+ * and merge items of hy_paged_decode_merge; no workspace). Returns
+ * HY_ENOSPACE when hy_decode_workspace_bytes(n_slots, num_q_heads, head_dim)
+ * exceeds HY_NOALLOC_SCRATCH_BYTES. Each GPU holds one array for the life of
+ * the process, shared by every call on that GPU and keeping the last call's
+ * contents: calls that overlap on one GPU (several streams or threads) race.
+ */
+int hy_paged_decode_append_noalloc(
+    const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
+    int64_t q_stride_head, void *q_out, int64_t qo_stride_seq,
+    int64_t qo_stride_tok, int64_t qo_stride_head, const void *k,
+    int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
+    const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
+    int64_t v_stride_head, const void *q_norm_weight,
+    const void *k_norm_weight, float eps, const float *cos_table,
+    const float *sin_table, int32_t max_positions, void *out,
+    int64_t o_stride_seq, int64_t o_stride_tok, int64_t o_stride_head,
+    void *k_pool, void *v_pool, int64_t pool_head_stride,
+    const int32_t *page_table, int64_t page_table_stride,
+    const int32_t *q_start, const int32_t *cache_lens,
+    const int32_t *decode_items, int32_t n_decode, const int32_t *merge_items,
+    int32_t n_merge, int32_t n_slots, int32_t num_seqs, int32_t num_q_heads,
+    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, float scale,
+    void *stream);
+
 /* (token, head) rows of one prefill query tile: hy_plan_tick cuts prefill
  * sequences into tiles of hy_prefill_tile_rows() / G tokens (G = query heads
  * per kv head), so callers size the prefill item list from it. Part of the
