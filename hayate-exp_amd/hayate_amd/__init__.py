@@ -5,7 +5,8 @@ for gfx950, C ABI in include/hayate_attn.h).
 """
 
 from .cache import Cache
-from .paged_cache import PagedCacheHandle, PagedKVBatch, PagedKVCacheManager
+from .paged_cache import PagedCacheHandle, PagedKVBatch, PagedKVCacheManager, PagedPrefix
+from .prefix_cache import PrefixCache, PrefixCacheMatch
 from .rope import compute_rope_params
 
 __all__ = [
@@ -13,5 +14,8 @@ __all__ = [
     "PagedCacheHandle",
     "PagedKVBatch",
     "PagedKVCacheManager",
+    "PagedPrefix",
+    "PrefixCache",
+    "PrefixCacheMatch",
     "compute_rope_params",
 ]

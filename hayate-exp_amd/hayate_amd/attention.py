@@ -1,17 +1,27 @@
 """Grouped-query attention module for the paged path.
 
-Same constructor and forward signature as the reference's
+Same constructor, parameters and forward signature as the reference's
 hayate/model/attention.py:17-122. In paged mode (the only mode Engine uses,
-engine.py:218-223) the projections stay torch GEMMs and everything between
-them runs in two HIP launches: the fused q/k RMSNorm + RoPE + KV append, then
-paged attention. The non-paged branch (contiguous history / varlen flash,
-attention.py:78-117) is not part of this library and raises.
+engine.py:218-223):
+
+* the three projections (attention.py:58-60) run as one GEMM against the
+  concatenated q/k/v weight, and q, k and v are strided views of its output
+  that the fused append kernel reads in place (no split copies);
+* q/k RMSNorm, RoPE and the paged K/V append (attention.py:62-75) are one
+  HIP launch, and paged attention another (a decode tick does both in one
+  launch plus the merge);
+* the kernels write the context as (B, T, Hq, D), so the reshape before
+  o_proj (attention.py:118-120) is a view.
+
+The non-paged branch (contiguous history / varlen flash, attention.py:78-117)
+is not part of this library and raises.
 """
 
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 
 class GroupedQueryAttention(nn.Module):
@@ -28,6 +38,32 @@ class GroupedQueryAttention(nn.Module):
         self.o_proj = nn.Linear(num_heads * head_dim, d_in, bias=False, dtype=dtype)
         self.q_norm = nn.RMSNorm(head_dim, eps=1e-6, dtype=dtype)
         self.k_norm = nn.RMSNorm(head_dim, eps=1e-6, dtype=dtype)
+        self._qkv_key = None
+        self._qkv_weight = None
+
+    def fused_qkv_weight(self) -> torch.Tensor:
+        """cat(q_proj.weight, k_proj.weight, v_proj.weight) along the output
+        dim, rebuilt whenever one of them is replaced or modified in place
+        (checkpoint loading copies into the parameters)."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
+        key = tuple((w.data_ptr(), w._version, w.device, w.dtype) for w in ws)
+        if key != self._qkv_key:
+            with torch.no_grad():
+                self._qkv_weight = torch.cat([w.detach() for w in ws], dim=0)
+            self._qkv_key = key
+        return self._qkv_weight
+
+    def project_qkv(self, x):
+        """x (B, T, d_in) -> q (B, T, Hq, D), k, v (B, T, Hkv, D): strided views
+        of one GEMM output (row stride (Hq + 2 Hkv) * D)."""
+        B, T, _ = x.shape
+        hq = self.num_heads * self.head_dim
+        hkv = self.num_kv_groups * self.head_dim
+        y = F.linear(x, self.fused_qkv_weight())
+        q = y[..., :hq].view(B, T, self.num_heads, self.head_dim)
+        k = y[..., hq : hq + hkv].view(B, T, self.num_kv_groups, self.head_dim)
+        v = y[..., hq + hkv :].view(B, T, self.num_kv_groups, self.head_dim)
+        return q, k, v
 
     def forward(
         self,
@@ -51,11 +87,9 @@ class GroupedQueryAttention(nn.Module):
                 "only the paged attention path is provided (pass paged_cache)"
             )
         B, T, _ = x.shape
-        q = self.q_proj(x).view(B, T, self.num_heads, self.head_dim)
-        k = self.k_proj(x).view(B, T, self.num_kv_groups, self.head_dim)
-        v = self.v_proj(x).view(B, T, self.num_kv_groups, self.head_dim)
-        q_norm_w = self.q_norm.weight if self.q_norm.weight is not None else None
-        k_norm_w = self.k_norm.weight if self.k_norm.weight is not None else None
+        q, k, v = self.project_qkv(x)
+        q_norm_w = self.q_norm.weight
+        k_norm_w = self.k_norm.weight
         eps = self.q_norm.eps if self.q_norm.eps is not None else torch.finfo(torch.float32).eps
         if paged_cache.varlen:
             # Varlen ticks carry packed tokens: x is (1, N, d_in).

@@ -48,6 +48,59 @@ class PagedCacheHandle:
     released: bool = False
 
 
+class PagedPrefix:
+    """The first `length` tokens of a cache as references to its physical
+    pages: the zero-copy form of a prefix snapshot (the reference gathers a
+    compact copy, paged_cache.py:180-190, and clones it again for the prefix
+    cache, prefix_cache.py:72).
+
+    Holding a PagedPrefix keeps its pages alive (one reference each).
+    Shared pages are copy-on-write for every handle that appends into them,
+    so the tokens a PagedPrefix covers never change: it is as immutable as
+    the reference's cloned Cache. It offers the part of the Cache interface
+    the prefix cache and the engine use (``length``, ``capacity``,
+    ``slice``, ``reset``); ``to_cache()`` gathers a compact Cache copy.
+    """
+
+    __slots__ = ("manager", "pages", "_length")
+
+    def __init__(self, manager: "PagedKVCacheManager", pages: list[int], length: int):
+        # the caller has already taken one reference per page for this object
+        self.manager = manager
+        self.pages = pages
+        self._length = length
+
+    @property
+    def length(self) -> int:
+        return self._length
+
+    @property
+    def capacity(self) -> int:
+        return self._length
+
+    def slice(self, end: int, clone: bool = False) -> "PagedPrefix":
+        """The first `end` tokens, sharing the pages (clone or not: shared
+        pages are never written, so a slice is already independent)."""
+        if end < 0:
+            raise ValueError("cache slice end must be non-negative")
+        if end > self._length:
+            raise ValueError(f"cache slice end {end} exceeds cache length {self._length}")
+        pages = self.pages[: -(-end // self.manager.page_size)]
+        self.manager._ref_pages(pages)
+        return PagedPrefix(self.manager, list(pages), end)
+
+    def reset(self) -> None:
+        """Drop the page references (idempotent)."""
+        if self.pages:
+            self.manager._drop_pages(self.pages)
+        self.pages = []
+        self._length = 0
+
+    def to_cache(self) -> Cache:
+        """A compact (layers, Hkv, length, D) copy gathered from the pages."""
+        return self.manager._gather(self.pages, self._length)
+
+
 def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -605,6 +658,10 @@ class PagedKVCacheManager:
             self._refs[p] = 1
         return pages
 
+    def _ref_pages(self, pages: Sequence[int]) -> None:
+        for p in pages:
+            self._refs[p] += 1
+
     def _drop_pages(self, pages: Sequence[int]) -> None:
         for p in pages:
             self._refs[p] -= 1
@@ -648,11 +705,20 @@ class PagedKVCacheManager:
             )
         handle.pages.extend(self._take_pages(missing))
 
-    def allocate_for_request(self, cache: Cache | None = None) -> PagedCacheHandle:
-        """Allocate a handle and optionally import a contiguous prefix (142-151)."""
+    def allocate_for_request(self, cache: "Cache | PagedPrefix | None" = None) -> PagedCacheHandle:
+        """Allocate a handle and optionally import a prefix (142-151): a
+        contiguous Cache is copied into fresh pages; a PagedPrefix is
+        shared without a copy (its pages gain a reference)."""
         handle = self.allocate()
         try:
-            if cache is not None and cache.length:
+            if isinstance(cache, PagedPrefix):
+                if cache.manager is not self:
+                    raise ValueError("a PagedPrefix belongs to the pool that made it")
+                if cache.length:
+                    self._ref_pages(cache.pages)
+                    handle.pages = list(cache.pages)
+                    handle.length = cache.length
+            elif cache is not None and cache.length:
                 self.import_cache(handle, cache)
         except Exception:
             self.release(handle)
@@ -701,12 +767,28 @@ class PagedKVCacheManager:
         snapshot_len = handle.length if length is None else length
         if snapshot_len < 0 or snapshot_len > handle.length:
             raise ValueError("snapshot length must be within the current cache length")
+        return self._gather(handle.pages, snapshot_len)
+
+    def share(self, handle: PagedCacheHandle, length: int | None = None) -> PagedPrefix:
+        """Zero-copy snapshot: the first `length` tokens (default: all) as a
+        PagedPrefix that references the handle's pages. Later appends by
+        the handle copy a shared page first, so the prefix never changes."""
+        if handle.released:
+            raise RuntimeError("cannot snapshot a released cache handle")
+        share_len = handle.length if length is None else length
+        if share_len < 0 or share_len > handle.length:
+            raise ValueError("snapshot length must be within the current cache length")
+        pages = handle.pages[: -(-share_len // self.page_size)]
+        self._ref_pages(pages)
+        return PagedPrefix(self, list(pages), share_len)
+
+    def _gather(self, page_list: Sequence[int], snapshot_len: int) -> Cache:
         _require_hip(self.k_cache, "snapshot")
         shape = (self.num_layers, self.num_kv_heads, snapshot_len, self.head_dim)
         k = torch.empty(shape, dtype=self.k_cache.dtype, device=self.device)
         v = torch.empty_like(k)
         if snapshot_len:
-            pages = torch.tensor(handle.pages, dtype=torch.int32, device=self.device)
+            pages = torch.tensor(list(page_list), dtype=torch.int32, device=self.device)
             for pool, dst in ((self.k_cache, k), (self.v_cache, v)):
                 rc = _native.lib().hy_page_gather(
                     pool.data_ptr(), pool.stride(0), pool.stride(2), pages.data_ptr(),
@@ -747,21 +829,19 @@ class PagedKVCacheManager:
 
     # -------------------------------------------------------------- sharing
     def fork(self, handle: PagedCacheHandle, length: int | None = None) -> PagedCacheHandle:
-        """New handle whose first `length` tokens (whole pages, default: all
-        full pages of `handle`) reference the same physical pages. Shared
-        pages are read-only; the first append into one copies it."""
+        """New handle whose first `length` tokens (default: all of them)
+        reference the same physical pages, a partly filled last page
+        included. Shared pages are read-only; the first append into one (by
+        either handle) copies it."""
         if handle.released:
             raise RuntimeError("cannot fork a released cache handle")
         if length is None:
-            length = handle.length // self.page_size * self.page_size
+            length = handle.length
         if length < 0 or length > handle.length:
             raise ValueError("fork length must be within the current cache length")
-        if length % self.page_size:
-            raise ValueError("fork length must be a whole number of pages")
         child = self.allocate()
-        shared = handle.pages[: length // self.page_size]
-        for p in shared:
-            self._refs[p] += 1
+        shared = handle.pages[: -(-length // self.page_size)]
+        self._ref_pages(shared)
         child.pages = list(shared)
         child.length = length
         return child

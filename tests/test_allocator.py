@@ -119,21 +119,59 @@ def test_commit_requires_reserved_space():
     assert h.length == 1
 
 
-def test_fork_shares_full_pages_and_refcounts():
+def test_fork_shares_pages_and_refcounts():
     m = make_manager(max_cache_tokens=16, max_requests=4)
     parent = m.allocate()
     m.reserve(parent, 5)
     parent.length = 5
-    child = m.fork(parent)  # whole pages only: 4 tokens, 2 pages
-    assert child.length == 4 and child.pages == parent.pages[:2]
-    assert [m.page_refcount(p) for p in parent.pages] == [2, 2, 1]
+    child = m.fork(parent)  # all 5 tokens: 3 pages, the last one partly filled
+    assert child.length == 5 and child.pages == parent.pages
+    assert [m.page_refcount(p) for p in parent.pages] == [2, 2, 2]
+    half = m.fork(parent, 3)  # 3 tokens: the first 2 pages
+    assert half.length == 3 and half.pages == parent.pages[:2]
+    assert [m.page_refcount(p) for p in parent.pages] == [3, 3, 2]
     with pytest.raises(ValueError):
-        m.fork(parent, 3)  # not a page boundary
+        m.fork(parent, 6)
     m.release(parent)
-    assert [m.page_refcount(p) for p in child.pages] == [1, 1]
-    assert m.free_page_count == 8 - 2
+    m.release(half)
+    assert [m.page_refcount(p) for p in child.pages] == [1, 1, 1]
+    assert m.free_page_count == 8 - 3
     m.release(child)
     assert m.free_page_count == 8
+
+
+def test_shared_prefix_references_pages_without_copies():
+    """share() / PagedPrefix / allocate_for_request(prefix): the zero-copy
+    path of the prefix cache is pure page bookkeeping."""
+    m = make_manager(max_cache_tokens=16, max_requests=4)
+    owner = m.allocate()
+    m.reserve(owner, 5)
+    owner.length = 5
+    prefix = m.share(owner, 4)
+    assert prefix.length == 4 and prefix.pages == owner.pages[:2]
+    assert [m.page_refcount(p) for p in owner.pages] == [2, 2, 1]
+    part = prefix.slice(3, clone=True)
+    assert part.length == 3 and part.pages == owner.pages[:2]
+    assert [m.page_refcount(p) for p in owner.pages] == [3, 3, 1]
+    with pytest.raises(ValueError):
+        prefix.slice(5)
+    req = m.allocate_for_request(part)  # no copy: the request shares the pages
+    assert req.length == 3 and req.pages == owner.pages[:2]
+    assert [m.page_refcount(p) for p in owner.pages] == [4, 4, 1]
+    part.reset()
+    part.reset()  # idempotent
+    prefix.reset()
+    m.release(owner)
+    assert [m.page_refcount(p) for p in req.pages] == [1, 1]
+    assert m.free_page_count == 8 - 2
+    m.release(req)
+    assert m.free_page_count == 8
+    # a prefix only attaches to the pool its pages belong to
+    h = m.allocate()
+    m.reserve(h, 2)
+    h.length = 2
+    with pytest.raises(ValueError):
+        make_manager().allocate_for_request(m.share(h))
 
 
 def test_claim_pages_takes_specific_free_pages():

@@ -91,13 +91,11 @@ class OraclePools:
 
 
 def expected_layer(mod, x, pools, layer, tables, page_lists, cache_lens, q_lens):
-    """Projections of x by the module's own linears, then the oracle's
+    """Projections of x by the module's own fused q/k/v GEMM, then the oracle's
     norm + rope + append (advancing the host pools) and attention.
     Returns the (N, HQ, D) context."""
     with torch.inference_mode():
-        q = mod.q_proj(x)
-        k = mod.k_proj(x)
-        v = mod.v_proj(x)
+        q, k, v = mod.project_qkv(x)
     n = sum(q_lens)
     q_rot = R.qknorm_rope_append(
         bits(q).reshape(n, HQ, D), bits(k).reshape(n, HKV, D), bits(v).reshape(n, HKV, D),

@@ -1,0 +1,170 @@
+"""The engine (hayate_amd/engine.py) on the GPU, checked layer by layer.
+
+A small Qwen3-shaped model (Qwen3-4B attention heads: 32 q / 8 kv, head_dim
+128; hidden 4096, 3 layers, vocab 512, random weights) runs real scheduler
+ticks: prompt chunks of up to 512 tokens and decode tokens in one varlen
+batch per tick, greedy sampling, commit, release. Layer 1's o_proj is the
+identity, so its attention module returns the context itself; on every tick
+a hook records that layer's input, its pool before and after the layer and
+its output, and the test replays the layer through the oracle (fused q/k/v
+projection by the module, then norm + rope + append + attention): pools bit
+for bit, context within the attention tolerances.
+
+The prefix-cache test checks that a hit shares the prompt's pages (no
+gather, no scatter: refcounts instead), that the first append into the
+shared partial page copies it, and that the request attends correctly.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import EPS, assert_attention_close, bits, say
+from oracle import paged_ref as R
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from hayate_amd.engine import Engine, Request
+    from hayate_amd.model import Qwen3Config
+
+    CFG = Qwen3Config(vocab_size=512, hidden_size=4096, num_layers=3, num_heads=32,
+                      num_kv_groups=8, head_dim=128, intermediate_size=1024)
+
+CHECK = 1
+HQ, HKV, D = 32, 8, 128
+
+
+def make_engine(**kw):
+    eng = Engine(config=CFG, seed=3, max_cache_tokens=16_384, max_batch_size=8,
+                 stop_token_ids=set(), **kw)
+    with torch.no_grad():
+        eng.model.layers[CHECK].self_attn.o_proj.weight.copy_(
+            torch.eye(HQ * D, dtype=torch.bfloat16))
+    g = torch.Generator(device=eng.device).manual_seed(4)
+    eng.paged_cache.k_cache.normal_(generator=g)
+    eng.paged_cache.v_cache.normal_(generator=g)
+    return eng
+
+
+class LayerProbe:
+    """Records (x, batch, pools before, pools after, output) of one
+    layer's attention module on every forward."""
+
+    def __init__(self, eng):
+        self.eng = eng
+        self.records = []
+        attn = eng.model.layers[CHECK].self_attn
+        self._pre = attn.register_forward_pre_hook(self.before)
+        self._post = attn.register_forward_hook(self.after)
+
+    def pools(self):
+        torch.cuda.synchronize()
+        m = self.eng.paged_cache
+        return bits(m.k_cache[CHECK, 0]), bits(m.v_cache[CHECK, 0])
+
+    def before(self, mod, args):
+        batch = args[7]
+        pages = [[int(p) for p in row if p >= 0] for row in batch._table_np]
+        self.records.append({"x": args[0].detach().clone(), "pre": self.pools(),
+                             "q_lens": list(batch.q_lens),
+                             "cache_lens": list(batch.cache_lens_host), "pages": pages})
+
+    def after(self, mod, args, out):
+        rec = self.records[-1]
+        rec["post"] = self.pools()
+        rec["y"] = out[0].detach().clone()
+
+    def check_all(self, tables):
+        mod = self.eng.model.layers[CHECK].self_attn
+        for i, rec in enumerate(self.records):
+            pk, pv = rec["pre"][0].copy(), rec["pre"][1].copy()
+            with torch.inference_mode():
+                q, k, v = mod.project_qkv(rec["x"])
+            n = sum(rec["q_lens"])
+            q_rot = R.qknorm_rope_append(
+                bits(q).reshape(n, HQ, D), bits(k).reshape(n, HKV, D),
+                bits(v).reshape(n, HKV, D), bits(mod.q_norm.weight), bits(mod.k_norm.weight),
+                EPS, tables[0], tables[1], pk, pv, rec["pages"], rec["cache_lens"],
+                rec["q_lens"], 128)
+            ctx = R.paged_attention(q_rot, pk, pv, rec["pages"], rec["cache_lens"],
+                                    rec["q_lens"], 128)
+            what = f"forward {i} q_lens={rec['q_lens']} cache={rec['cache_lens']}"
+            assert np.array_equal(rec["post"][0], pk), f"{what}: K pool"
+            assert np.array_equal(rec["post"][1], pv), f"{what}: V pool"
+            assert_attention_close(bits(rec["y"]).reshape(n, HQ, D), ctx, what)
+        self.records.clear()
+
+
+def tables_of(eng):
+    return eng.model.cos.cpu().numpy(), eng.model.sin.cpu().numpy()
+
+
+def prompt(seed, n):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, CFG.vocab_size, (n,), generator=g).tolist()
+
+
+def test_engine_ticks_match_the_oracle_layer_by_layer():
+    say("[engine: 3 requests, chunked prefill + decode, layer 1 vs oracle]")
+    eng = make_engine()
+    probe = LayerProbe(eng)
+    tables = tables_of(eng)
+    reqs = []
+    for i, n in enumerate((700, 300, 50)):
+        r = Request(id=i, prompt_tokens=prompt(10 + i, n), max_tokens=4)
+        eng.add_request(r)
+        reqs.append(r)
+    shapes = []
+    while eng.generate():
+        shapes.append((eng.last_tick.prefill_tokens, eng.last_tick.decode_tokens))
+        probe.check_all(tables)
+    say(f"  ticks (prefill, decode tokens): {shapes}")
+    # tick 1: chunks 512 + 300 + 50; tick 2: A's last 188 + two decodes; ...
+    assert shapes[0] == (862, 0) and shapes[1] == (188, 2)
+    assert len(shapes) >= 4 and all(p == 0 for p, _ in shapes[2:])
+    for r in reqs:
+        assert r.is_completed and len(r.tokens) == 4
+        assert r.paged_cache is None  # released after completion
+    assert eng.paged_cache.free_page_count == eng.paged_cache.num_pages
+
+
+def test_prefix_cache_hit_shares_pages():
+    say("[engine: prefix-cache hit shares pages]")
+    eng = make_engine(enable_prefix_cache=True, prefix_cache_max_tokens=4096)
+    probe = LayerProbe(eng)
+    tables = tables_of(eng)
+    tokens = prompt(20, 300)
+    first = Request(id=0, prompt_tokens=list(tokens), max_tokens=3)
+    eng.add_request(first)
+    eng.generate()  # prefill: the prompt's pages go to the prefix cache
+    probe.check_all(tables)
+    assert not first.is_prefill and len(eng.prefix_cache) == 1
+    owner_pages = list(first.paged_cache.pages)
+    m = eng.paged_cache
+    assert [m.page_refcount(p) for p in owner_pages] == [2, 2, 2]
+
+    def forbidden(*a, **k):
+        raise AssertionError("a prefix hit must not gather or scatter")
+
+    m.import_cache = forbidden
+    m._gather = forbidden
+    second = Request(id=1, prompt_tokens=list(tokens), max_tokens=3)
+    eng.add_request(second)  # hit: 299 tokens (max_prefix_len = len - 1)
+    assert second.kv_cache.length == 299
+    eng.generate()  # first decodes; second prefills one token at position 299
+    probe.check_all(tables)
+    pages = second.paged_cache.pages
+    assert pages[:2] == owner_pages[:2], "full prompt pages are shared"
+    assert pages[2] != owner_pages[2], "the partial page was copied on write"
+    assert m.page_refcount(owner_pages[0]) == 3  # first, the cache entry, second
+    # the copied page holds the prompt's keys (the shared tokens 256..298)
+    k = m.k_cache[:, 0]
+    assert torch.equal(k[:, :, pages[2] * 128 : pages[2] * 128 + 43].view(torch.int16),
+                       k[:, :, owner_pages[2] * 128 : owner_pages[2] * 128 + 43]
+                       .view(torch.int16))
+    while eng.generate():
+        probe.check_all(tables)
+    assert first.is_completed and second.is_completed
+    eng.clear_prefix_cache()
+    assert m.free_page_count == m.num_pages

@@ -123,9 +123,7 @@ def test_attention_module_paged_forward():
     x = torch.randn(3, T, d_in, device=DEV, dtype=torch.bfloat16)
     with torch.inference_mode():
         y, nk, nv = mod(x, cos, sin, None, None, None, paged_cache=batch, layer_idx=1)
-        qp = mod.q_proj(x).view(3, T, hq, d)
-        kp = mod.k_proj(x).view(3, T, hkv, d)
-        vp = mod.v_proj(x).view(3, T, hkv, d)
+        qp, kp, vp = mod.project_qkv(x)
     torch.cuda.synchronize()
     assert nk is None and nv is None
     pk, pv = pre_k.copy(), pre_v.copy()

@@ -1,0 +1,38 @@
+"""Host-side pieces of the attention module and model that run without a
+GPU: the fused q/k/v projection and the checkpoint name map."""
+
+import torch
+
+from hayate_amd.attention import GroupedQueryAttention
+from hayate_amd.model import Qwen3Config, Qwen3Model, qwen_weight_map
+
+
+def test_fused_qkv_projection_views_one_gemm():
+    torch.manual_seed(0)
+    mod = GroupedQueryAttention(64, 4, 2, 16, dtype=torch.float32)
+    x = torch.randn(3, 5, 64)
+    q, k, v = mod.project_qkv(x)
+    torch.testing.assert_close(q, mod.q_proj(x).view(3, 5, 4, 16))
+    torch.testing.assert_close(k, mod.k_proj(x).view(3, 5, 2, 16))
+    torch.testing.assert_close(v, mod.v_proj(x).view(3, 5, 2, 16))
+    # views of one buffer: no split copies, rows 16-byte aligned
+    base = q.untyped_storage().data_ptr()
+    assert k.untyped_storage().data_ptr() == base == v.untyped_storage().data_ptr()
+    assert q.stride() == (5 * 128, 128, 16, 1) and k.stride(1) == 128
+    # the fused weight follows in-place updates of the parameters
+    with torch.no_grad():
+        mod.k_proj.weight.mul_(2)
+    _, k2, _ = mod.project_qkv(x)
+    torch.testing.assert_close(k2, 2 * k)
+
+
+def test_checkpoint_name_map_covers_every_parameter():
+    cfg = Qwen3Config(vocab_size=64, hidden_size=32, num_layers=2, num_heads=4,
+                      num_kv_groups=2, head_dim=8, intermediate_size=48)
+    with torch.device("meta"):
+        model = Qwen3Model(cfg)
+    names = qwen_weight_map(model)
+    params = {id(p) for p in model.parameters()}
+    assert {id(p) for p in names.values()} == params
+    assert "model.layers.1.self_attn.q_norm.weight" in names
+    assert len(names) == 3 + 11 * 2
