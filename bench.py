@@ -7,16 +7,24 @@ in [256, 4096], 262,144-token pool); consecutive steps use different layers
 of an 8-layer pool, as the 36 layers of a forward pass do, so the 256 MB
 MALL cannot serve the K/V bytes. value = algorithmic bytes of a step
 (every K/V row of every context once + q/out rows + appended rows) divided
-by the measured step time, in GB/s. The K timed steps are captured as one
-HIP graph and replayed (a serving engine replays its captured forward pass
-the same way); the eager time of the same steps, with the host's launch
-work between kernels, is reported beside it.
+by the step time, in GB/s. The K timed steps are captured as one HIP graph
+and replayed (a serving engine replays its captured forward pass the same
+way); the reported step time is the median over replays. The eager time of
+the same steps (median of per-step HIP events) is reported beside it.
 
-The JSON line also carries the other four workloads (GPU timing only), the
-roofline of the dominant kernel (decode attention; its average duration is
-measured with HIP events on the launch stream over the timed steps) and a
-CPU baseline: the oracle's decode attention timed on the host, one thread,
-on a bounded sample of the same workload.
+The JSON line also carries
+* the other four workloads (GPU timing; medians over >= 20 steps);
+* "roofline" for the decode kernel and "roofline_prefill" for the prefill
+  kernel: each kernel's median duration from HIP events recorded on its
+  launch stream around every launch of the timed steps ("source" says so;
+  the committed rocprofv3 summaries under profiles/ give the kernel-only
+  durations and the HBM traffic / MFMA counters);
+* "engine": 36-layer Qwen3-4B ticks (synthetic weights) through
+  hayate_amd.engine's model, eager and as a replayed graph, with the share
+  of the tick spent in the attention kernels;
+* "cpu_baseline": the reference's CPU attention path (paged write +
+  compiled FlexAttention over the physical-page block mask, restated in
+  oracle/flex_ref.py) on the host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
@@ -26,6 +34,8 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import platform
+import statistics
 import sys
 import time
 
@@ -45,6 +55,10 @@ def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
+def median(xs):
+    return float(statistics.median(xs)) if xs else None
+
+
 def step_fn(w, batch, layer, decode_only):
     """One step: the fused q/k norm + RoPE + append of the step's tokens,
     then attention. A batch of decode tokens runs both in one launch
@@ -59,10 +73,37 @@ def step_fn(w, batch, layer, decode_only):
 
 
 DECODE_KERNELS = ("hy_paged_decode", "hy_paged_decode_append")
+TIMED_KERNELS = DECODE_KERNELS + ("hy_paged_prefill", "hy_paged_decode_merge",
+                                  "hy_paged_prefill_merge")
 
 
-def time_workload(name, steps, warmup, layers, split=0):
-    """Times `steps` steps; returns a dict of measurements."""
+class KernelEvents:
+    """HIP events around each launch of the named C calls, on the launch
+    stream (a PagedKVBatch.launch_hook)."""
+
+    def __init__(self, names, stream, capacity):
+        self.stream = stream
+        self.pool = {n: [(torch.cuda.Event(enable_timing=True),
+                          torch.cuda.Event(enable_timing=True)) for _ in range(capacity)]
+                     for n in names}
+        self.used = {n: 0 for n in names}
+
+    def __call__(self, name, after):
+        if name not in self.pool or self.used[name] >= len(self.pool[name]):
+            return
+        pair = self.pool[name][self.used[name]]
+        pair[1 if after else 0].record(self.stream)
+        if after:
+            self.used[name] += 1
+
+    def medians_ms(self):
+        return {n: median([a.elapsed_time(b) for a, b in self.pool[n][: self.used[n]]])
+                for n in self.pool if self.used[n]}
+
+
+def time_workload(name, steps, warmup, layers, split=0, replays=5):
+    """Times `steps` steps eagerly (per-step events) and as `replays`
+    replays of one captured K-step graph; returns a dict of medians."""
     from hayate_amd.workloads import make_workload
 
     w = make_workload(name, device="cuda", num_layers=layers, tokens_per_split=split)
@@ -75,72 +116,52 @@ def time_workload(name, steps, warmup, layers, split=0):
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(steps)]
-    # events bracketing the attention kernels, created before the timed region
-    timed = DECODE_KERNELS + ("hy_paged_prefill",)
-    pool = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                for _ in range(steps)] for n in timed}
-    used = {n: 0 for n in timed}
-
-    def hook(kname, after):
-        if kname in pool:
-            pair = pool[kname][used[kname]]
-            pair[1 if after else 0].record(stream)
-            if after:
-                used[kname] += 1
-
-    batch.launch_hook = hook
+    kev = KernelEvents(TIMED_KERNELS, stream, steps)
+    batch.launch_hook = kev
     t0 = time.perf_counter()
     for i in range(steps):
-        layer = i % layers
         ev[i][0].record(stream)
-        step_fn(w, batch, layer, decode_only)
+        step_fn(w, batch, i % layers, decode_only)
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     batch.launch_hook = None
-    step_events_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
-    step_ms = (t1 - t0) * 1e3 / steps
-    kernel_ms = {n: float(np.mean([a.elapsed_time(b) for a, b in pool[n][: used[n]]]))
-                 for n in timed if used[n]}
+    kernel_ms = kev.medians_ms()
     dec_kernel = next((n for n in DECODE_KERNELS if n in kernel_ms), None)
     out = {
         "workload": w.spec.description,
-        "ms_per_step": step_ms,
-        "step_events_ms": step_events_ms,
+        "ms_per_step_eager": median([a.elapsed_time(b) for a, b in ev]),
+        "ms_per_step_eager_wall": (t1 - t0) * 1e3 / steps,
         "decode_bytes": w.decode_bytes(),
         "decode_kernel_bytes": w.decode_bytes(include_append=decode_only),
         "prefill_flops": w.prefill_flops(),
         "n_decode_items": plan.n_decode,
         "n_prefill_items": plan.n_prefill,
-        "kernel_ms": kernel_ms,
+        "kernel_ms_median": kernel_ms,
         "decode_kernel": dec_kernel,
     }
+    out.update(time_graphs(w, batch, steps, layers, decode_only, replays))
+    step_ms = out["ms_per_step_graph"]
     if out["decode_bytes"]:
-        out["decode_GBps_step"] = out["decode_bytes"] / (step_ms * 1e-3) / 1e9
+        out["decode_GBps_graph"] = out["decode_bytes"] / (step_ms * 1e-3) / 1e9
         if dec_kernel and not out["prefill_flops"]:
             out["decode_GBps_kernel"] = (out["decode_kernel_bytes"]
                                          / (kernel_ms[dec_kernel] * 1e-3) / 1e9)
     if out["prefill_flops"]:
-        out["prefill_TFLOPs_events"] = out["prefill_flops"] / (step_events_ms * 1e-3) / 1e12
+        out["prefill_TFLOPs_graph"] = out["prefill_flops"] / (step_ms * 1e-3) / 1e12
         if "hy_paged_prefill" in kernel_ms and not out["decode_bytes"]:
             out["prefill_TFLOPs_kernel"] = (out["prefill_flops"]
                                             / (kernel_ms["hy_paged_prefill"] * 1e-3) / 1e12)
-    out.update(time_graphs(w, batch, steps, layers, decode_only))
-    if out["decode_bytes"]:
-        out["decode_GBps_graph"] = out["decode_bytes"] / (out["ms_per_step_graph"] * 1e-3) / 1e9
-    if out["prefill_flops"]:
-        out["prefill_TFLOPs_graph"] = (out["prefill_flops"]
-                                       / (out["ms_per_step_graph"] * 1e-3) / 1e12)
     del w, batch
     torch.cuda.empty_cache()
     return out
 
 
-def time_graphs(w, batch, steps, layers, decode_only):
-    """The same K steps captured as one HIP graph (a serving engine captures
-    its forward pass over the layer stack the same way) and replayed: the
-    step time without the host's per-launch work between kernels. One
-    untimed replay first; then one timed replay of exactly K steps."""
+def time_graphs(w, batch, steps, layers, decode_only, replays):
+    """The same K steps captured as one HIP graph and replayed: the step
+    time without the host's per-launch work between kernels. One untimed
+    replay, then `replays` timed replays (events on the replay stream);
+    the median replay / K is the step time."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -154,47 +175,204 @@ def time_graphs(w, batch, steps, layers, decode_only):
             step_fn(w, batch, i % layers, decode_only)
     g.replay()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    g.replay()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
+    stream = torch.cuda.current_stream()
+    times = []
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) / steps)
     del g
-    return {"ms_per_step_graph": (t1 - t0) * 1e3 / steps}
+    return {"ms_per_step_graph": median(times), "graph_replays": replays}
 
 
-def cpu_baseline(budget_s=10.0):
-    """Oracle decode attention on the host, 1 thread, over the batch-32
-    decode workload: whole passes over its 32 requests until about
-    `budget_s` seconds of work are done."""
-    from threadpoolctl import threadpool_limits
+# ----------------------------------------------------------------- engine
+def time_engine(steps, warmup, which):
+    """36-layer Qwen3-4B forward ticks (synthetic weights) through
+    hayate_amd.engine's model on one begin_tick batch: "decode" = the
+    batch-32 decode workload's requests (one token each), "mixed" = the
+    mixed-tick workload's 8 x 512 prefill chunks + 56 decode tokens. The
+    requests' histories are placed on random pages of a random-filled pool
+    (the prefill that would have produced them is not run). The same
+    batch is replayed each step (the appended rows overwrite themselves).
+    Reports the tick time eager (median of per-tick events) and as a
+    replayed graph, tokens per second, and the median share of the eager
+    tick spent inside the attention launches."""
+    import math
 
-    from hayate_amd.workloads import make_workload
-    from oracle import paged_ref as R
+    from hayate_amd.engine import Engine
+    from hayate_amd.model import Qwen3Config
+    from hayate_amd.workloads import _lengths, SPECS
 
-    w = make_workload("decode_b32", device="cuda", num_layers=1)
-    pk = R.torch_bf16_to_bits(w.manager.k_cache[0, 0])
-    pv = R.torch_bf16_to_bits(w.manager.v_cache[0, 0])
-    q = R.torch_bf16_to_bits(w.q)
-    del w.manager
+    gen = torch.Generator().manual_seed(SPECS["decode_b32" if which == "decode" else
+                                             "mixed_tick"].seed)
+    cache_lens, q_lens = _lengths("decode_b32" if which == "decode" else "mixed_tick", gen)
+    pages = sum(math.ceil((c + q) / 128) for c, q in zip(cache_lens, q_lens))
+    eng = Engine(config=Qwen3Config(), seed=0, max_cache_tokens=(pages + 64) * 128,
+                 max_batch_size=len(q_lens), stop_token_ids=set())
+    m = eng.paged_cache
+    g = torch.Generator(device=m.device).manual_seed(5)
+    m.k_cache.normal_(generator=g)
+    m.v_cache.normal_(generator=g)
+    handles = []
+    for c in cache_lens:
+        h = m.allocate()
+        m.reserve(h, c)
+        h.length = c
+        handles.append(h)
+    batch = m.begin_tick(handles, q_lens)
+    ids = torch.randint(0, eng.model.config.vocab_size, (1, sum(q_lens)),
+                        generator=torch.Generator().manual_seed(6)).to(m.device)
+    stream = torch.cuda.current_stream()
+
+    def fwd():
+        with torch.inference_mode():
+            return eng.model(ids, paged_cache=batch)[0]
+
+    for _ in range(warmup):
+        fwd()
+    torch.cuda.synchronize()
+    n_layers = eng.num_layers
+    names = TIMED_KERNELS + ("hy_qknorm_rope_append",)
+    ticks, shares = [], []
+    for _ in range(steps):
+        kev = KernelEvents(names, stream, n_layers)
+        batch.launch_hook = kev
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fwd()
+        b.record(stream)
+        torch.cuda.synchronize()
+        batch.launch_hook = None
+        tick = a.elapsed_time(b)
+        attn = sum(x.elapsed_time(y) for n in names for x, y in kev.pool[n][: kev.used[n]])
+        ticks.append(tick)
+        shares.append(attn / tick)
+    # graph: one captured tick, replayed
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        fwd()
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fwd()
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = []
+    for _ in range(max(5, steps // 2)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        replays.append(a.elapsed_time(b))
+    n_tok = sum(q_lens)
+    out = {
+        "model": "Qwen3-4B (36 layers, hidden 2560, 32 q / 8 kv heads, synthetic weights)",
+        "tick": (f"{len(q_lens)} decode tokens (batch-32 decode contexts)" if which == "decode"
+                 else "8 x 512 prefill chunks + 56 decode tokens (mixed-tick lengths)"),
+        "tokens_per_tick": n_tok,
+        "ms_per_tick_eager": median(ticks),
+        "ms_per_tick_graph": median(replays),
+        "tokens_per_s_graph": n_tok / (median(replays) * 1e-3),
+        "attention_share_eager": median(shares),
+    }
+    del graph, batch, eng, m
     torch.cuda.empty_cache()
-    done_bytes = 0
-    passes = 0
-    torch.set_num_threads(1)
-    with threadpool_limits(limits=1):
+    return out
+
+
+# ------------------------------------------------------------ CPU baseline
+def cpu_info():
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model, os.cpu_count(), len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(names, runs=3):
+    """The reference's CPU attention path for each named workload, on the
+    host's cores: the paged write of the step's K/V rows and compiled
+    FlexAttention over the physical-page block mask (oracle/flex_ref.py).
+    One warm-up call (it includes Inductor's compile, reported apart), then
+    the median of `runs` calls. Mixed ticks run as the reference runs them:
+    one forward per equal-length group (engine.py:257-261, 303-312)."""
+    from hayate_amd.workloads import make_workload
+    from oracle import flex_ref as F
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    model, logical, affinity = cpu_info()
+    rows = {}
+    for name in names:
+        w = make_workload(name, device="cpu", fill=False)
+        g = torch.Generator().manual_seed(w.spec.seed + 7)
+        cap = w.manager.capacity_tokens
+        kp = w.manager.k_cache[0].normal_(generator=g)  # (1, Hkv, capacity, D)
+        vp = w.manager.v_cache[0].normal_(generator=g)
+        groups = {}
+        start = 0
+        for i, ql in enumerate(w.q_lens):
+            groups.setdefault(ql, []).append((i, start))
+            start += ql
+        calls = []
+        for ql, members in groups.items():
+            idx = [i for i, _ in members]
+            sel = torch.cat([torch.arange(s, s + ql) for _, s in members])
+            q = w.q[sel].view(len(idx), ql, 32, 128).transpose(1, 2).contiguous()
+            k = w.k[sel].view(len(idx), ql, 8, 128).transpose(1, 2).contiguous()
+            v = w.v[sel].view(len(idx), ql, 8, 128).transpose(1, 2).contiguous()
+            fb = F.FlexPagedBatch([w.page_lists[i] for i in idx],
+                                  [w.cache_lens[i] for i in idx], ql, 128, cap)
+            calls.append((fb, q, k, v))
+
+        def once():
+            for fb, q, k, v in calls:
+                fb.write_layer(kp, vp, k, v)
+                fb.attend_layer(q, kp, vp)
+
         t0 = time.perf_counter()
-        while time.perf_counter() - t0 < budget_s:
-            R.paged_attention(q, pk, pv, w.page_lists, w.cache_lens, w.q_lens, 128,
-                              dtype=np.float32)
-            done_bytes += w.decode_bytes()
-            passes += 1
-        dt = time.perf_counter() - t0
+        once()
+        first = time.perf_counter() - t0
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            once()
+            times.append(time.perf_counter() - t0)
+        t = median(times)
+        row = {"ms": round(t * 1e3, 3), "first_call_incl_compile_s": round(first, 2),
+               "runs": runs, "forwards": len(calls)}
+        if w.decode_bytes():
+            row["decode_GBps"] = round(w.decode_bytes() / t / 1e9, 3)
+        if w.prefill_flops():
+            row["prefill_TFLOPs"] = round(w.prefill_flops() / t / 1e12, 4)
+        rows[name] = row
+        log(f"[bench] cpu {name}: {row}")
+        del w, kp, vp, calls, once
+    head = rows.get("decode_b32") or next(iter(rows.values()))
     return {
-        "value": round(done_bytes / dt / 1e9, 3),
+        "value": head.get("decode_GBps"),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"oracle float32 paged decode attention, {passes} passes over the 32 requests "
-                  f"of the batch-32 decode workload ({dt:.1f} s, one thread)",
+        "sample": ("the reference's CPU path restated (paged write + torch.compile'd "
+                   "flex_attention over the physical-page BlockMask, oracle/flex_ref.py), "
+                   f"decode_b32 at full size, median of {runs} calls after one warm-up "
+                   "call that includes the compile; per-workload rows in 'configs'"),
+        "cpu_model": model,
+        "logical_cpus": logical,
+        "threads": threads,
+        "configs": rows,
     }
 
 
@@ -202,13 +380,17 @@ def traffic_from_profile(name):
     """HBM bytes per launch of the dominant kernel, read from the committed
     rocprofv3 --pmc summary profiles/<name>.md (FETCH_SIZE + WRITE_SIZE,
     each calibrated against a plain 1 GiB copy), or None."""
+    return _profile_value(name, "hbm_bytes_per_launch", int)
+
+
+def _profile_value(name, key, cast):
     path = os.path.join(ROOT, "profiles", f"{name}.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         for line in f:
-            if line.startswith("hbm_bytes_per_launch ="):
-                return int(line.split("=", 1)[1])
+            if line.startswith(key + " ="):
+                return cast(line.split("=", 1)[1])
     return None
 
 
@@ -221,6 +403,9 @@ def main():
     ap.add_argument("--split", type=int, default=0, help="decode tokens per split (0 = auto)")
     ap.add_argument("--only", default="", help="comma-separated workloads (default: all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-configs", default="decode_b1,decode_b32",
+                    help="workloads timed on the CPU path (comma-separated, or 'all')")
+    ap.add_argument("--no-engine", action="store_true", help="skip the 36-layer engine ticks")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -244,6 +429,7 @@ def main():
         log(f"[bench] {name}: {json.dumps(results[name])}")
 
     head = results["decode_b32"]
+    dk = head["decode_kernel"]
     line = {
         "metric": METRIC,
         "value": round(head["decode_GBps_graph"], 1),
@@ -260,26 +446,51 @@ def main():
         "config": {
             "workload": "decode_b32: batched paged decode, batch 32, contexts U[256, 4096], "
                         "262,144-token pool, 128-token pages, 32 q / 8 kv heads, head_dim 128; "
-                        f"step = qk-norm+rope+append fused into decode attention (one launch) "
-                        f"+ merge, {args.layers} layers rotated; the K timed steps replay as one "
-                        "HIP graph",
-            "ms_per_step_eager": round(head["ms_per_step"], 5),
+                        "step = qk-norm+rope+append fused into decode attention (one launch) "
+                        f"+ merge, {args.layers} layers rotated; step time = median over "
+                        f"replays of one captured graph of the {args.steps} timed steps",
+            "ms_per_step_eager": round(head["ms_per_step_eager"], 5),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"decode_kernel<4, fused append> ({head['decode_kernel']})",
+            "kernel": f"decode_kernel<4, fused append> ({dk})",
             "achieved": round(head["decode_GBps_kernel"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(head["decode_GBps_kernel"] / HBM_PEAK_GBS, 4),
-            "kernel_us": round(head["kernel_ms"][head["decode_kernel"]] * 1e3, 2),
+            "kernel_us": round(head["kernel_ms_median"][dk] * 1e3, 2),
+            "source": "median of HIP events around each launch on its stream (includes the "
+                      "dispatch latency; rocprofv3 kernel-only durations are in profiles/)",
             "algorithmic_bytes": head["decode_kernel_bytes"],
             "traffic": traffic_from_profile("decode_kernel_decode_b32"),
         },
     }
+    pre = results.get("prefill_4x512")
+    if pre and "prefill_TFLOPs_kernel" in pre:
+        line["roofline_prefill"] = {
+            "bound": "mfma",
+            "kernel": "prefill_kernel<4, 64> (hy_paged_prefill) on prefill_4x512",
+            "achieved": round(pre["prefill_TFLOPs_kernel"], 1),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(pre["prefill_TFLOPs_kernel"] / BF16_PEAK_TFLOPS, 4),
+            "kernel_us": round(pre["kernel_ms_median"]["hy_paged_prefill"] * 1e3, 2),
+            "flops": pre["prefill_flops"],
+            "source": "median of HIP events around each launch on its stream",
+            "step_TFLOPs_graph": round(pre["prefill_TFLOPs_graph"], 1),
+            "mfma_util": _profile_value("prefill_kernel_prefill_4x512", "mfma_util", float),
+        }
+    if not args.no_engine:
+        line["engine"] = {}
+        for which in ("decode", "mixed"):
+            log(f"[bench] engine {which}")
+            line["engine"][which] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                     for k, v in time_engine(args.steps, 3, which).items()}
+            log(f"[bench] engine {which}: {line['engine'][which]}")
     if not args.no_cpu:
         log("[bench] cpu baseline")
-        line["cpu_baseline"] = cpu_baseline()
+        cpu_names = ORDER if args.cpu_configs == "all" else args.cpu_configs.split(",")
+        line["cpu_baseline"] = cpu_baseline(cpu_names)
     line["configs"] = {
         n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
         for n, r in results.items()
