@@ -32,13 +32,27 @@
 //                 read instruction serves 32 lanes (four rows x 64 bytes)
 //                 per LDS cycle; a 320-byte row pitch (80 dwords, 16 mod 64
 //                 banks) puts those four rows on disjoint banks.
-// K/V tiles of KEYS keys are double buffered in LDS: the next tile is loaded
-// into registers while the current one is computed, then stored, then one
-// barrier. The softmax rescales lazily: the exponent base of a row only
+// K/V tiles of KEYS keys are double buffered in LDS and filled by gfx950's
+// 16-byte direct-to-LDS loads (global_load_lds_dwordx4): the next tile's
+// loads go out at the start of a tile and land in the other buffer without
+// passing through registers; one wait and one barrier per tile. A load
+// instruction writes 64 lanes x 16 bytes to consecutive LDS addresses, so
+// the bank-conflict-free layouts are lane permutations instead of padded
+// rows (16-byte units, "chunk" = 8 dims):
+//   K: unit(row, chunk) = (row / 16) * 256 + chunk * 16 + row % 16. The
+//      K-operand read (16 lanes = 16 rows, one chunk) touches 16
+//      consecutive units; one load instruction = 16 rows x 4 chunks
+//      (64-byte runs of each row).
+//   V: unit(row, chunk) = (row / 4) * 64 + chunk * 4 + row % 4. The
+//      transposing read (32 lanes = 4 rows x 32 dims) touches 16
+//      consecutive units; one load instruction = 4 whole rows.
+// Both give per-lane base addresses with compile-time offsets for every
+// block, dim slice and row group. The softmax rescales lazily: the exponent
+// base of a row only
 // moves when its max grows by more than 2^8, so the accumulators are rarely
 // touched by VALU. Key blocks past the causal limit of every row of a wave
 // are skipped by that wave.
-// Rows at or past kv_end are filled from the last valid key, so masked
+// Rows at or past kv_end are loaded from the last valid key, so masked
 // scores never meet NaN bits of unwritten rows.
 //
 // A split whose item has slot >= 0 writes an fp32 partial (unnormalised
@@ -61,10 +75,7 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRows = kPrefillRows;  // (token, head) rows per workgroup
 constexpr int kThreads = 2 * kRows;  // one wave per 32 rows
-constexpr int kKRow = 136;     // u16 per K row in LDS (272 bytes)
-constexpr int kVRow = 160;     // u16 per V row in LDS (320 bytes)
 constexpr float kLazy = 8.0f;  // rescale threshold, exp2 domain
-constexpr int kTileKeys = kPrefillTileKeys;  // keys per LDS stage
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -81,6 +92,34 @@ __device__ __forceinline__ s16x4 tr_read(const uint16_t *p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(const_cast<uint16_t *>(p)));
 }
 
+// 16 bytes from global memory straight into LDS: lane l's bytes land at
+// lds + 16 l (lds is wave-uniform and goes to M0). Inline assembly, so the
+// compiler neither orders LDS reads behind these writes nor waits for them:
+// the kernel waits explicitly (wait_tile_loads) before the barrier that
+// publishes a tile, and never reads a buffer that loads are filling.
+__device__ __forceinline__ void load_to_lds(const uint16_t *g, const uint16_t *lds) {
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) uint16_t *)lds));
+  // M0 has no other user in this kernel (no LDS-DMA builtins, no indexed
+  // register access), so setting it here disturbs nothing.
+  __asm__ volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                   :
+                   : "v"(g), "s"(__builtin_amdgcn_readfirstlane(m0))
+                   : "memory");
+}
+
+// Waits until this wave's outstanding vector-memory loads (the direct-to-LDS
+// tile loads), LDS reads and scalar loads (the page-table lookups) have all
+// completed: s_waitcnt vmcnt(0) lgkmcnt(0), expcnt left alone (simm16 0x0070).
+// Issued through the builtin, the compiler's own wait tracking sees it, so
+// it knows no scalar load is pending in the block loop that follows and can
+// wait there for single LDS reads (a pending scalar load, which may return
+// out of order, would force it to wait for every LDS read).
+__device__ __forceinline__ void wait_tile_loads() {
+  __builtin_amdgcn_s_waitcnt(0x0070);
+  __asm__ volatile("" ::: "memory");
+}
+
 // v_permlane32_swap with both operands x: the first result holds, in every
 // lane, x of lane l % 32 and the second x of lane 32 + l % 32, so combining
 // the two gives the same value in both lanes of a row.
@@ -95,9 +134,17 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int G, int KEYS>
-__global__ __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(kPrefillWgPerCu * kThreads / 256, kPrefillWgPerCu * kThreads / 256)))
+constexpr int kTile = 64;                        // keys per LDS stage (two blocks)
+constexpr int kStage = 2 * kTile * kHeadDim;     // halfs per stage: K tile, then V tile
+constexpr int kStages = 3;                       // ring of stages (96 KiB)
+
+// Instruction classes for __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedValu = 0x002 | 0x400;  // VALU incl. transcendentals
+constexpr int kSchedDsRead = 0x100;
+
+template <int G>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
     uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
@@ -106,12 +153,8 @@ void prefill_kernel(
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ kv_lens,
     const int32_t *__restrict__ items, float *__restrict__ ws_acc, float *__restrict__ ws_ml,
     int num_kv_heads, int page_shift, float scale_log2) {
-  static_assert(KEYS % 32 == 0 && KEYS >= 32, "tiles are whole 32-key blocks");
-  constexpr int kChunks = KEYS * 16 / kThreads;  // 16-byte K (and V) chunks per thread
-  constexpr int kPass = kThreads / 16;            // tile rows one chunk index covers
-  static_assert(KEYS * 16 % kThreads == 0 && kPass % 16 == 0, "staging covers whole rows");
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][KEYS * kKRow];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][KEYS * kVRow];
+  static_assert(kThreads == 512, "eight waves");
+  __shared__ __attribute__((aligned(1024))) uint16_t smem[kStages * kStage];
 
   const int32_t *it = items + 8 * blockIdx.y;
   const int kvh = blockIdx.x;
@@ -138,13 +181,18 @@ void prefill_kernel(
   const bool live = row_tok < q_end;
   bf16x8 qop[8];
   {
+    // rows past the chunk read the chunk's first row (in bounds) and are
+    // zeroed, so the eight loads issue together without a branch
     const uint16_t *src = q + seq * q_ss +
                           static_cast<int64_t>(qs + (live ? row_tok : q_begin)) * q_st +
                           (h0 + r % G) * q_sh;
+    u32x4 raw[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) raw[kk] = load16(src + 16 * kk + 8 * h);
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (live) w = load16(src + 16 * kk + 8 * h);
+      u32x4 w = raw[kk];
+      if (!live) w = u32x4{0u, 0u, 0u, 0u};
       qop[kk] = __builtin_bit_cast(bf16x8, w);
       // Scores come out of the MFMA in exp2 units: q * scale * log2(e),
       // rounded to bf16 once here.
@@ -186,84 +234,123 @@ void prefill_kernel(
   const bool wave_live = tw0 < q_end;
   const int wave_lo = min(cache_len + tw0, last_key);
   const int wave_hi = min(cache_len + tw1, last_key);
+  // This wave computes the item's 32-key blocks [0, nb); blocks from jm on
+  // cross its rows' diagonal and are masked.
+  const int nb = wave_live && wave_hi >= kv_begin ? (wave_hi - kv_begin) / 32 + 1 : 0;
+  const int jm = wave_lo >= kv_begin ? (wave_lo - kv_begin + 1) / 32 : 0;
 
   const uint16_t *kh = k_pool + kvh * pool_hs;
   const uint16_t *vh = v_pool + kvh * pool_hs;
   const int32_t *pt = page_table + seq * pt_stride;
   const int page_mask = (1 << page_shift) - 1;
+  const int n_tiles = (kv_end - kv_begin + kTile - 1) / kTile;
 
-  // Staging: thread t moves chunk j < kChunks of the K and of the V tile:
-  // row kPass j + t / 16, dims 8 (t % 16) .. +7. A 32-row group lies in one
-  // page: one wave-uniform page lookup per chunk. Rows at or past kv_end
-  // read the last valid key instead (any finite data: their scores are
-  // masked), so the loads need no branch.
-  const int srow = tid >> 4;
-  const int scol = (tid & 15) * 8;
-  // Page ids of a tile's chunks (scalar loads), fetched one tile before the
-  // tile's loads so that no wave waits for them.
+  // Tile loads: wave w issues K instructions 2w, 2w + 1 (rows 16 (w / 2) +
+  // lane % 16, chunks 4 (i % 4) + lane / 16) and V instructions 2w, 2w + 1
+  // (rows 4 i + lane % 4, chunk lane / 4). A wave's rows lie in one page
+  // (pages hold >= 32 keys), so each tensor needs one page id per tile;
+  // they are fetched a tile ahead. Rows at or past kv_end load the last
+  // valid key (any finite data: their scores are masked).
   struct Pages {
-    int32_t id[kChunks];
+    int32_t k, v;
   };
   auto fetch_pages = [&](int kt) __attribute__((always_inline)) {
     Pages pg;
-#pragma unroll
-    for (int j = 0; j < kChunks; ++j)
-      pg.id[j] = pt[min(kt + ((kPass * j) & ~31), last_key) >> page_shift];
+    pg.k = pt[min(kt + 16 * (wave >> 1), last_key) >> page_shift];
+    pg.v = pt[min(kt + 8 * wave, last_key) >> page_shift];
     return pg;
   };
-  auto load_tile = [&](int kt, const Pages &pg, u32x4(&kr)[kChunks], u32x4(&vr)[kChunks])
-                       __attribute__((always_inline)) {
+  auto issue_tile = [&](int kt, const Pages &pg, uint16_t *dst) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
-      const int key = min(kt + kPass * j + srow, last_key);
-      const int64_t p = (static_cast<int64_t>(pg.id[j]) << page_shift) + (key & page_mask);
-      kr[j] = load16(kh + p * kHeadDim + scol);
-      vr[j] = load16(vh + p * kHeadDim + scol);
-    }
-  };
-  auto store_tile = [&](int b, const u32x4(&kr)[kChunks], const u32x4(&vr)[kChunks])
-                        __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
-      *reinterpret_cast<u32x4 *>(&sK[b][(kPass * j + srow) * kKRow + scol]) = kr[j];
-      *reinterpret_cast<u32x4 *>(&sV[b][(kPass * j + srow) * kVRow + scol]) = vr[j];
+    for (int j = 0; j < 2; ++j) {
+      const int i = 2 * wave + j;
+      {
+        const int key = min(kt + 16 * (i >> 2) + (lane & 15), last_key);
+        const int64_t p = (static_cast<int64_t>(pg.k) << page_shift) + (key & page_mask);
+        load_to_lds(kh + p * kHeadDim + 8 * (4 * (i & 3) + (lane >> 4)), dst + i * 512);
+      }
+      {
+        const int key = min(kt + 4 * i + (lane & 3), last_key);
+        const int64_t p = (static_cast<int64_t>(pg.v) << page_shift) + (key & page_mask);
+        load_to_lds(vh + p * kHeadDim + 8 * (lane >> 2), dst + kTile * kHeadDim + i * 512);
+      }
     }
   };
 
-  // Per-lane LDS bases: K operand row c, dims 8 h; V^T transposed read: row
-  // 4 (q16 / 2) + r16 / 4 of the key quad, dims 16 (q16 % 2) + 4 (r16 % 4).
+  // Per-lane LDS read bases (u16 units). K operand of row c, dims 16 kk +
+  // 8 h: unit (c / 16) * 256 + (2 kk + h) * 16 + c % 16, i.e. base + 256 kk.
+  // V^T transposed read of lane (q16, r16): row 4 (q16 / 2) + r16 / 4 (+ 8
+  // for the second half, + 16 kh2, + 32 kb), dims 16 (q16 % 2) + 4 (r16 % 4)
+  // (+ 32 db), i.e. base + 1024 hi + 2048 kh2 + 128 db.
   const int r16 = lane & 15;
   const int q16 = lane >> 4;
-  const int k_base = c * kKRow + 8 * h;
-  const int v_base = (4 * (q16 >> 1) + (r16 >> 2)) * kVRow + 16 * (q16 & 1) + 4 * (r16 & 3);
+  const int k_base = (c >> 4) * 2048 + h * 128 + (c & 15) * 8;
+  const int v_base = 512 * (q16 >> 1) + 64 * (q16 & 1) + 32 * ((r16 & 3) >> 1) + 8 * (r16 >> 2) +
+                     4 * (r16 & 1);
+  // Block j's K and V rows in the ring: stage (j / 2) % 3, half j % 2.
+  auto k_block = [&](int j) -> const uint16_t * {
+    return smem + ((j >> 1) % kStages) * kStage + 4096 * (j & 1) + k_base;
+  };
+  auto v_block = [&](int j) -> const uint16_t * {
+    return smem + ((j >> 1) % kStages) * kStage + kTile * kHeadDim + 4096 * (j & 1) + v_base;
+  };
 
-  // One 32-key block starting at key kb0, K/V rows at Kb/Vb in LDS.
-  auto block = [&](auto masked, const uint16_t *Kb, const uint16_t *Vb, int kb0)
-                   __attribute__((always_inline)) {
-    constexpr bool kMasked = decltype(masked)::value;
+  // Software pipeline over this wave's blocks. Block j's body runs the
+  // QK^T MFMAs of block j + 1 while the VALU does block j's softmax (the
+  // two are independent), then block j + 1's base shift, then block j's
+  // P V MFMAs; K operands are read two blocks ahead and V operands at the
+  // start of their block, so no LDS read is waited for right after it is
+  // issued. The scores a block's softmax sees were shifted by the base at
+  // the time of its QK^T, and the base only moves in the softmax (before
+  // the next shift), so scores and base always agree.
+  bf16x8 kop[8];
+  auto read_k = [&](int j) __attribute__((always_inline)) {
+    const uint16_t *kb = k_block(j);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) kop[kk] = *reinterpret_cast<const bf16x8 *>(kb + 256 * kk);
+  };
+  auto qk = [&]() __attribute__((always_inline)) {
     f32x16 s;
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const bf16x8 kop = *reinterpret_cast<const bf16x8 *>(Kb + k_base + 16 * kk);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop, qop[kk], s, 0, 0, 0);
-    }
-    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s, 0, 0, 0);
-    if constexpr (kMasked) {
+    for (int kk = 0; kk < 8; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop[kk], qop[kk], s, 0, 0, 0);
+    return s;
+  };
+
+  // Softmax of one block's scores s (relative to r_mma): lane (c, h) holds
+  // row c's scores for keys 8 (i / 4) + 4 h + i % 4 of the block.
+  // probs(): the common case, straight-line code the scheduler can
+  // interleave with the next block's QK^T MFMAs: probabilities against the
+  // current base, packed to bf16, their sum and the row max. rebase(): when
+  // some row's max exceeds the base by more than kLazy (or a row sees its
+  // first key) the base moves and the block's probabilities are redone
+  // (rare).
+  auto mask = [&](f32x16 &s, int kb0) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
-        if (key > limit) s[i] = -INFINITY;
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb0 + 8 * (i >> 2) + 4 * h + (i & 3);
+      s[i] = key > limit ? -INFINITY : s[i];
     }
-    float mx = fmaxf(s[0], s[1]);
+  };
+  auto probs = [&](const f32x16 &s, bf16x8 &pop0, bf16x8 &pop1, float &psum, float &mx)
+                   __attribute__((always_inline)) {
+    psum = 0.f;
+    mx = s[0];
 #pragma unroll
-    for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    for (int i = 0; i < 16; ++i) {
+      if (i) mx = fmaxf(mx, s[i]);
+      const float p = __builtin_amdgcn_exp2f(s[i]);
+      psum += p;
+      if (i < 8)
+        pop0[i] = static_cast<__bf16>(p);
+      else
+        pop1[i - 8] = static_cast<__bf16>(p);
+    }
+  };
+  auto rebase = [&](const f32x16 &s, float mx, bf16x8 &pop0, bf16x8 &pop1, float &psum)
+                    __attribute__((always_inline)) {
     mx = halves_max(mx);  // row max relative to r_mma
-    // The base only moves when the row max exceeds it by more than kLazy
-    // (from -inf: at the first visible key), so probabilities stay below
-    // 2^kLazy; the new base is the row max.
     const bool need = base == -INFINITY ? mx != -INFINITY : mx > kLazy;
     if (__builtin_expect(__any(need), 0)) {
       const float r_new = need ? mx + r_mma : r_mma;
@@ -273,11 +360,19 @@ void prefill_kernel(
         base = r_new;
         r_mma = r_new;
       }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] -= delta;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+      psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = __builtin_amdgcn_exp2f(s[i] - delta);
+        psum += p;
+        if (i < 8)
+          pop0[i] = static_cast<__bf16>(p);
+        else
+          pop1[i - 8] = static_cast<__bf16>(p);
+      }
       const float hi = __uint_as_float(f32_to_bf16_rne(r_mma) << 16);
       const float mid = __uint_as_float(f32_to_bf16_rne(r_mma - hi) << 16);
       const float lo = r_mma - hi - mid;  // at most 8 significant bits left
@@ -285,79 +380,95 @@ void prefill_kernel(
       shift_b[1] = static_cast<__bf16>(h == 0 ? -mid : 0.0f);
       shift_b[2] = static_cast<__bf16>(h == 0 ? -lo : 0.0f);
     }
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float p = __builtin_amdgcn_exp2f(s[i]);
-      s[i] = p;
-      psum += p;
-    }
     l_run += psum;
-    const bf16x8 pop0 = pack8(s, 0);
-    const bf16x8 pop1 = pack8(s, 8);
+  };
+  // V^T operands of block j (eight 32-dim x 16-key slices), then P V.
+  s16x8 vop[8];
+  auto read_v = [&](int j, int half) __attribute__((always_inline)) {
+    const uint16_t *vb = v_block(j);
+#pragma unroll
+    for (int db = 2 * half; db < 2 * half + 2; ++db)
+#pragma unroll
+      for (int kh2 = 0; kh2 < 2; ++kh2) {
+        const s16x4 lo = tr_read(vb + 2048 * kh2 + 128 * db);
+        const s16x4 hi = tr_read(vb + 2048 * kh2 + 128 * db + 1024);
+        vop[2 * db + kh2] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+  };
+  auto pv = [&](const bf16x8 &pop0, const bf16x8 &pop1) __attribute__((always_inline)) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int kh2 = 0; kh2 < 2; ++kh2) {
-        const uint16_t *vp = Vb + v_base + 16 * kh2 * kVRow + 32 * db;
-        const s16x4 lo = tr_read(vp);
-        const s16x4 hi = tr_read(vp + 8 * kVRow);
-        const s16x8 v8 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, v8),
-                                                          kh2 ? pop1 : pop0, acc[db], 0, 0, 0);
-      }
+      for (int kh2 = 0; kh2 < 2; ++kh2)
+        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, vop[2 * db + kh2]), kh2 ? pop1 : pop0, acc[db], 0, 0, 0);
   };
 
-  const int n_tiles = (kv_end - kv_begin + KEYS - 1) / KEYS;
-  {
-    u32x4 kr[kChunks], vr[kChunks];
-    load_tile(kv_begin, fetch_pages(kv_begin), kr, vr);
-    store_tile(0, kr, vr);
-  }
-  Pages pg_next = {};
-  if (n_tiles > 1) pg_next = fetch_pages(kv_begin + KEYS);
-  __syncthreads();
-
-  // Tiles whose keys every live row of the workgroup sees need no mask
-  // (they come first); the rest decide per wave and 32-key block whether to
-  // skip, compute plainly or mask.
-  int n_plain = (min(cache_len + q_begin, last_key) + 1 - kv_begin) / KEYS;
-  n_plain = n_plain < 0 ? 0 : (n_plain > n_tiles ? n_tiles : n_plain);
-  auto iterate = [&](auto diag, int t) __attribute__((always_inline)) {
-    constexpr bool kDiag = decltype(diag)::value;
-    const int kt = kv_begin + KEYS * t;
-    const int b = t & 1;
-    const bool has_next = t + 1 < n_tiles;
-    u32x4 kr[kChunks], vr[kChunks];
-    if (has_next) {
-      load_tile(kt + KEYS, pg_next, kr, vr);
-      if (t + 2 < n_tiles) pg_next = fetch_pages(kt + 2 * KEYS);
-    }
-    if (wave_live) {
+  // One block: half of block j's V reads go out first (the LDS counter
+  // holds at most 15 outstanding reads, so the first MFMA's wait for the K
+  // operands cannot leave all 16 in flight); then QK^T of block j + 1 on the
+  // matrix core, interleaved with the other V reads and block j's
+  // probabilities (one MFMA, one LDS read, six VALU instructions, eight
+  // times); then the rare rebase, block j + 1's base shift, the K reads of
+  // block j + 2 and block j's P V.
+  f32x16 s_cur;
+  auto body = [&](bool masked, int j) __attribute__((always_inline)) {
+    bf16x8 pop0, pop1;
+    float psum, mx;
+    if (masked) mask(s_cur, kv_begin + 32 * j);  // blocks on the diagonal
+    read_v(j, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 s_nxt = qk();
+    read_v(j, 1);
+    probs(s_cur, pop0, pop1, psum, mx);
 #pragma unroll
-      for (int kb = 0; kb < KEYS / 32; ++kb) {
-        const uint16_t *Kb = sK[b] + 32 * kb * kKRow;
-        const uint16_t *Vb = sV[b] + 32 * kb * kVRow;
-        const int kb0 = kt + 32 * kb;
-        if constexpr (!kDiag) {
-          block(std::false_type{}, Kb, Vb, kb0);
-        } else {
-          if (kb0 <= wave_hi) {
-            if (kb0 + 31 <= wave_lo)
-              block(std::false_type{}, Kb, Vb, kb0);
-            else
-              block(std::true_type{}, Kb, Vb, kb0);
-          }
-        }
-      }
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 6, 0);
     }
-    if (has_next) {
-      store_tile(b ^ 1, kr, vr);
+    // the probabilities count as used here, so the compiler keeps them in
+    // this straight-line region instead of sinking them past the rebase test
+    __asm__ volatile("" ::"v"(psum), "v"(pop0), "v"(pop1));
+    __builtin_amdgcn_sched_barrier(0);
+    rebase(s_cur, mx, pop0, pop1, psum);
+    s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_nxt, 0, 0, 0);
+    read_k(j + 2);
+    pv(pop0, pop1);
+    s_cur = s_nxt;
+  };
+
+  // Prologue: tiles 0 and 1 in flight, then block 0's scores and block 1's
+  // K operands.
+  if (n_tiles > 0) issue_tile(kv_begin, fetch_pages(kv_begin), smem);
+  if (n_tiles > 1) issue_tile(kv_begin + kTile, fetch_pages(kv_begin + kTile), smem + kStage);
+  Pages pg_next = {};
+  if (n_tiles > 2) pg_next = fetch_pages(kv_begin + 2 * kTile);
+  wait_tile_loads();
+  __syncthreads();
+  read_k(0);
+  s_cur = qk();
+  s_cur = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_cur, 0, 0, 0);
+  read_k(1);
+
+  // Tile t: tile t + 2's loads go into the stage tile t - 1 used (every wave
+  // left it before the last barrier), then this wave's blocks 2t, 2t + 1;
+  // the barrier publishes tile t + 2, which the K reads two blocks ahead
+  // need during tile t + 1. A block body always runs the next block's
+  // QK^T and K reads (past the wave's last block they read stale LDS and
+  // their results are dropped), so the body is one straight path.
+  for (int t = 0; t < n_tiles; ++t) {
+    if (t + 2 < n_tiles)
+      issue_tile(kv_begin + (t + 2) * kTile, pg_next, smem + ((t + 2) % kStages) * kStage);
+#pragma unroll 1
+    for (int j = 2 * t; j < min(2 * t + 2, nb); ++j) body(j >= jm, j);
+    if (t + 1 < n_tiles) {
+      // tile t + 3's page ids; the wait below covers them too
+      if (t + 3 < n_tiles) pg_next = fetch_pages(kv_begin + (t + 3) * kTile);
+      wait_tile_loads();
       __syncthreads();
     }
-  };
-  for (int t = 0; t < n_plain; ++t) iterate(std::false_type{}, t);
-  for (int t = n_plain; t < n_tiles; ++t) iterate(std::true_type{}, t);
+  }
 
   // Epilogue: full row sums, then the output or the split's partial.
   const float lsum = halves_sum(l_run);
@@ -474,7 +585,7 @@ void launch_prefill(hipStream_t st, int num_kv_heads, int n_items, const uint16_
                     int64_t pool_hs, const int32_t *page_table, int64_t pt_stride,
                     const int32_t *q_start, const int32_t *kv_lens, const int32_t *items,
                     float *ws_acc, float *ws_ml, int page_shift, float scale_log2) {
-  hipLaunchKernelGGL((prefill_kernel<G, kTileKeys>), dim3(num_kv_heads, n_items), dim3(kThreads), 0,
+  hipLaunchKernelGGL((prefill_kernel<G>), dim3(num_kv_heads, n_items), dim3(kThreads), 0,
                      st, q, q_ss,
                      q_st, q_sh, out, o_ss, o_st, o_sh, k_pool, v_pool, pool_hs, page_table,
                      pt_stride, q_start, kv_lens, items, ws_acc, ws_ml, num_kv_heads, page_shift,

@@ -201,6 +201,18 @@ def test_mixed_tick_small():
     _ragged([0, 700, 5, 1023, 64], [300, 1, 1, 40, 1])
 
 
+def test_prefill_deep_prefix_splits():
+    """One chunk over a 20,000-token prefix plus a shallow chunk: the deep
+    one's key range is split across workgroups (merged by the merge
+    launch), the shallow one runs whole."""
+    from hayate_amd import _native
+
+    p = _native.plan_tick(np.array([300, 40]), np.array([20_300, 100]), 32, 8, 128, 256, 0)
+    assert len(p.prefill_merge) > 0
+    assert all(int(r[5]) == -1 for r in p.prefill if int(r[0]) == 1)
+    _ragged([20_000, 60], [300, 40], pool_tokens=22_000)
+
+
 def test_page_size_256():
     _ragged([300, 0, 1000], [1, 70, 1], page_size=256)
 
