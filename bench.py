@@ -189,6 +189,26 @@ def time_graphs(w, batch, steps, layers, decode_only, replays):
 
 
 # ----------------------------------------------------------------- engine
+def engine_benchmark():
+    """The reference's benchmark method (benchmarks/cli.py:98-190) on the
+    engine, via hayate_amd.benchmark: prompt prefill of 512-token prompts
+    and 64 decode steps, median of 3 after a warm-up, at batch 1 (the CLI's
+    default) and batch 20 (the engine's default batch limit); synthetic
+    Qwen3-4B weights, eager execution."""
+    from hayate_amd import benchmark
+    from hayate_amd.engine import Engine
+    from hayate_amd.model import Qwen3Config
+
+    eng = Engine(config=Qwen3Config(), seed=0, max_batch_size=20)
+    out = {}
+    for b in (1, 20):
+        rows = benchmark.run(eng, batch_size=b, context_tokens=512, decode_steps=64,
+                             repetitions=3)
+        out[f"batch_{b}"] = [{k: (round(v, 3) if isinstance(v, float) else v)
+                              for k, v in r.items()} for r in rows]
+    return out
+
+
 def time_engine(steps, warmup, which):
     """36-layer Qwen3-4B forward ticks (synthetic weights) through
     hayate_amd.engine's model on one begin_tick batch: "decode" = the
@@ -487,6 +507,9 @@ def main():
             line["engine"][which] = {k: (round(v, 4) if isinstance(v, float) else v)
                                      for k, v in time_engine(args.steps, 3, which).items()}
             log(f"[bench] engine {which}: {line['engine'][which]}")
+        log("[bench] engine prefill/decode benchmark")
+        line["engine"]["benchmark"] = engine_benchmark()
+        log(f"[bench] engine benchmark: {line['engine']['benchmark']}")
     if not args.no_cpu:
         log("[bench] cpu baseline")
         cpu_names = ORDER if args.cpu_configs == "all" else args.cpu_configs.split(",")

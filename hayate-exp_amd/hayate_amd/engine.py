@@ -287,6 +287,29 @@ class Engine:
                 r.is_prefill = False
                 self._store_prompt_prefix(r)
 
+    def prefill_batch(self, requests: List[Request]) -> None:
+        """One prompt chunk per request, sampling the requests whose prompt is
+        done (engine.py:226-276). The reference runs one forward per group of
+        equal-length chunks; here all chunks go into one varlen tick."""
+        for r in requests:
+            if not r.prompt_tokens:
+                if self.tokenizer is None:
+                    raise ValueError("no tokenizer: give the request's prompt_tokens")
+                r.prompt_tokens = self.tokenizer.encode(r.prompt)
+            if not r.prompt_tokens:
+                raise ValueError("prompt must tokenize to at least one token")
+            if not r.is_prefill:
+                raise ValueError("prefill_batch needs requests whose prompt is not done")
+        if requests:
+            self.step(requests)
+
+    def decode_batch(self, requests: List[Request]) -> None:
+        """One token for every request from its latest token (engine.py:278-289)."""
+        if any(r.is_prefill for r in requests):
+            raise ValueError("decode_batch needs requests whose prompt is done")
+        if requests:
+            self.step(requests)
+
     def generate(self) -> bool:
         """One scheduler tick; False once no request is active (engine.py:291-314)."""
         previous = list(self.scheduler.current_batch)

@@ -168,3 +168,47 @@ def test_prefix_cache_hit_shares_pages():
     assert first.is_completed and second.is_completed
     eng.clear_prefix_cache()
     assert m.free_page_count == m.num_pages
+
+
+def test_prefill_batch_and_decode_batch_match_generate():
+    """The reference's call shapes (engine.py:226-289: prefill_batch until
+    every prompt is done, then decode_batch) give the tokens the scheduler
+    path gives; two requests of equal length keep every tick's shape the
+    same on both paths, so the tokens must agree exactly."""
+    say("[engine: prefill_batch / decode_batch against generate]")
+    prompts = [prompt(30, 700), prompt(31, 700)]
+    eng = make_engine()
+    ra = [Request(id=i, prompt_tokens=list(p), max_tokens=4) for i, p in enumerate(prompts)]
+    for r in ra:
+        eng.add_request(r)
+    while eng.generate():
+        pass
+    eng = make_engine()
+    rb = [Request(id=i, prompt_tokens=list(p), max_tokens=4) for i, p in enumerate(prompts)]
+    for r in rb:
+        eng._prepare_request(r)
+    pending = list(rb)
+    while pending:
+        eng.prefill_batch(pending)
+        pending = [r for r in pending if r.is_prefill]
+    with pytest.raises(ValueError):
+        eng.prefill_batch(rb)  # prompts done
+    while not all(r.is_completed for r in rb):
+        eng.decode_batch([r for r in rb if not r.is_completed])
+    assert [r.tokens for r in ra] == [r.tokens for r in rb]
+    assert all(len(r.tokens) == 4 for r in rb)
+
+
+def test_benchmark_reports_prefill_and_decode():
+    """hayate_amd.benchmark (the reference's benchmarks/cli.py method) on a
+    small run: both phases timed, every page returned afterwards."""
+    from hayate_amd import benchmark
+
+    say("[engine: benchmark.run]")
+    eng = make_engine()
+    rows = benchmark.run(eng, batch_size=2, context_tokens=200, decode_steps=3, repetitions=1)
+    assert [r["phase"] for r in rows] == ["prefill", "decode"]
+    assert rows[0]["tokens_per_second"] > 0 and rows[1]["tokens_per_second"] > 0
+    assert rows[1]["latency_ms_per_step"] > 0
+    say(f"  {rows}")
+    assert eng.paged_cache.free_page_count == eng.paged_cache.num_pages
