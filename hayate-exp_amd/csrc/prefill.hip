@@ -88,6 +88,24 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16 &s, int base) {
   return r;
 }
 
+__device__ __forceinline__ float tree_sum16(const float (&p)[16]) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = p[2 * i] + p[2 * i + 1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = a[2 * i] + a[2 * i + 1];
+  return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+__device__ __forceinline__ float tree_max16(const f32x16 &s) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = fmaxf(s[2 * i], s[2 * i + 1]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = fmaxf(a[2 * i], a[2 * i + 1]);
+  return fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+}
+
 __device__ __forceinline__ s16x4 tr_read(const uint16_t *p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(const_cast<uint16_t *>(p)));
 }
@@ -333,20 +351,21 @@ void prefill_kernel(
       s[i] = key > limit ? -INFINITY : s[i];
     }
   };
+  // Sums and maxima of a lane's 16 values are pairwise trees: four
+  // dependent steps instead of fifteen.
   auto probs = [&](const f32x16 &s, bf16x8 &pop0, bf16x8 &pop1, float &psum, float &mx)
                    __attribute__((always_inline)) {
-    psum = 0.f;
-    mx = s[0];
+    float p[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      if (i) mx = fmaxf(mx, s[i]);
-      const float p = __builtin_amdgcn_exp2f(s[i]);
-      psum += p;
+      p[i] = __builtin_amdgcn_exp2f(s[i]);
       if (i < 8)
-        pop0[i] = static_cast<__bf16>(p);
+        pop0[i] = static_cast<__bf16>(p[i]);
       else
-        pop1[i - 8] = static_cast<__bf16>(p);
+        pop1[i - 8] = static_cast<__bf16>(p[i]);
     }
+    psum = tree_sum16(p);
+    mx = tree_max16(s);
   };
   auto rebase = [&](const f32x16 &s, float mx, bf16x8 &pop0, bf16x8 &pop1, float &psum)
                     __attribute__((always_inline)) {
@@ -363,16 +382,16 @@ void prefill_kernel(
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-      psum = 0.f;
+      float p[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(s[i] - delta);
-        psum += p;
+        p[i] = __builtin_amdgcn_exp2f(s[i] - delta);
         if (i < 8)
-          pop0[i] = static_cast<__bf16>(p);
+          pop0[i] = static_cast<__bf16>(p[i]);
         else
-          pop1[i - 8] = static_cast<__bf16>(p);
+          pop1[i - 8] = static_cast<__bf16>(p[i]);
       }
+      psum = tree_sum16(p);
       const float hi = __uint_as_float(f32_to_bf16_rne(r_mma) << 16);
       const float mid = __uint_as_float(f32_to_bf16_rne(r_mma - hi) << 16);
       const float lo = r_mma - hi - mid;  // at most 8 significant bits left
@@ -411,14 +430,14 @@ void prefill_kernel(
   // probabilities (one MFMA, one LDS read, six VALU instructions, eight
   // times); then the rare rebase, block j + 1's base shift, the K reads of
   // block j + 2 and block j's P V.
-  f32x16 s_cur;
-  auto body = [&](bool masked, int j) __attribute__((always_inline)) {
+  f32x16 s_a, s_b;
+  auto body = [&](bool masked, int j, f32x16 &s_cur, f32x16 &s_nxt) __attribute__((always_inline)) {
     bf16x8 pop0, pop1;
     float psum, mx;
     if (masked) mask(s_cur, kv_begin + 32 * j);  // blocks on the diagonal
     read_v(j, 0);
     __builtin_amdgcn_sched_barrier(0);
-    f32x16 s_nxt = qk();
+    s_nxt = qk();
     read_v(j, 1);
     probs(s_cur, pop0, pop1, psum, mx);
 #pragma unroll
@@ -435,7 +454,6 @@ void prefill_kernel(
     s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_nxt, 0, 0, 0);
     read_k(j + 2);
     pv(pop0, pop1);
-    s_cur = s_nxt;
   };
 
   // Prologue: tiles 0 and 1 in flight, then block 0's scores and block 1's
@@ -447,8 +465,8 @@ void prefill_kernel(
   wait_tile_loads();
   __syncthreads();
   read_k(0);
-  s_cur = qk();
-  s_cur = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_cur, 0, 0, 0);
+  s_a = qk();
+  s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_a, 0, 0, 0);
   read_k(1);
 
   // Tile t: tile t + 2's loads go into the stage tile t - 1 used (every wave
@@ -460,8 +478,10 @@ void prefill_kernel(
   for (int t = 0; t < n_tiles; ++t) {
     if (t + 2 < n_tiles)
       issue_tile(kv_begin + (t + 2) * kTile, pg_next, smem + ((t + 2) % kStages) * kStage);
-#pragma unroll 1
-    for (int j = 2 * t; j < min(2 * t + 2, nb); ++j) body(j >= jm, j);
+    // two bodies per tile with the score registers swapped, so the
+    // next block's scores never have to be copied into place
+    if (2 * t < nb) body(2 * t >= jm, 2 * t, s_a, s_b);
+    if (2 * t + 1 < nb) body(2 * t + 1 >= jm, 2 * t + 1, s_b, s_a);
     if (t + 1 < n_tiles) {
       // tile t + 3's page ids; the wait below covers them too
       if (t + 3 < n_tiles) pg_next = fetch_pages(kv_begin + (t + 3) * kTile);
