@@ -18,8 +18,10 @@ seeded random ids otherwise. Stop tokens are disabled while measuring so
 every request produces its full token count.
 
 Run as ``python -m hayate_amd.benchmark [--model DIR] --batch-size B
---context-tokens N --decode-steps S``; without --model the engine uses
-synthetic Qwen3-4B weights.
+--context-tokens N --decode-steps S [--compile]``; without --model the
+engine uses synthetic Qwen3-4B weights; --compile replays decode ticks from
+captured HIP graphs (the reference's CLI flag of the same name compiles
+with torch.compile).
 """
 
 from __future__ import annotations
@@ -172,12 +174,16 @@ def main(argv: Optional[List[str]] = None) -> List[dict]:
     ap.add_argument("--context-tokens", type=_positive, default=512)
     ap.add_argument("--decode-steps", type=_positive, default=64)
     ap.add_argument("--repetitions", type=_positive, default=3)
+    ap.add_argument("--compile", action="store_true",
+                    help="replay decode ticks from captured HIP graphs")
+    ap.add_argument("--compile-mode", default="default")
     ap.add_argument("--max-cache-tokens", type=_positive, default=None,
                     help="pool size (default: enough for the batch, at least the engine's)")
     ap.add_argument("--json", type=Path, default=None)
     args = ap.parse_args(argv)
     need = args.batch_size * (args.context_tokens + args.decode_steps + DEFAULT_KV_PAGE_SIZE)
-    engine = Engine(args.model, max_batch_size=max(args.batch_size, MAX_BATCH_SIZE),
+    engine = Engine(args.model, args.compile, args.compile_mode,
+                    max_batch_size=max(args.batch_size, MAX_BATCH_SIZE),
                     max_cache_tokens=args.max_cache_tokens or max(need, DEFAULT_KV_CACHE_TOKENS))
     rows = run(engine, args.batch_size, args.context_tokens, args.decode_steps, args.repetitions)
     text = json.dumps(rows, indent=2)

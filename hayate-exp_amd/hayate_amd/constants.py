@@ -1,5 +1,9 @@
 """Engine constants kept from the reference (hayate/engine/constants.py:8-24)."""
 
+# Accepted compile modes (constants.py:5): on this path compile=True means
+# decode ticks replayed from captured HIP graphs, except in the last mode.
+COMPILE_MODES = ("default", "reduce-overhead", "max-autotune", "max-autotune-no-cudagraphs")
+
 # Requests admitted into one batch by the reference scheduler (constants.py:8).
 MAX_BATCH_SIZE = 20
 

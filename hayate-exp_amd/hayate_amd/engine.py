@@ -26,6 +26,7 @@ without one, requests carry ``prompt_tokens`` and responses stay token ids.
 
 from __future__ import annotations
 
+import json
 import os
 from dataclasses import dataclass, field
 from queue import Queue
@@ -34,11 +35,13 @@ from typing import List, Optional, Union
 import torch
 
 from .constants import (
+    COMPILE_MODES,
     DEFAULT_KV_CACHE_TOKENS,
     DEFAULT_KV_PAGE_SIZE,
     DEFAULT_PREFILL_CHUNK_SIZE,
     MAX_BATCH_SIZE,
 )
+from .decode_graph import DecodeGraphRunner
 from .model import Qwen3Config, Qwen3Model, init_synthetic_weights, load_local_weights
 from .paged_cache import PagedCacheHandle, PagedKVCacheManager, PagedPrefix
 from .prefix_cache import PrefixCache
@@ -101,21 +104,32 @@ class Engine:
     def __init__(
         self,
         model_dir: Optional[str] = None,
-        *,
-        config: Optional[Qwen3Config] = None,
-        seed: int = 0,
+        compile: bool = False,
+        compile_mode: str = "default",
         enable_prefix_cache: bool = False,
         prefix_cache_max_tokens: int = DEFAULT_PREFIX_CACHE_MAX_TOKENS,
         prefill_chunk_size: int = DEFAULT_PREFILL_CHUNK_SIZE,
         max_cache_tokens: int = DEFAULT_KV_CACHE_TOKENS,
         kv_page_size: int = DEFAULT_KV_PAGE_SIZE,
+        *,
+        config: Optional[Qwen3Config] = None,
+        seed: int = 0,
         max_batch_size: int = MAX_BATCH_SIZE,
         tokenizer=None,
         stop_token_ids: Optional[set[int]] = None,
         device: str = "cuda",
     ):
+        """Positional arguments follow the reference's Engine (engine.py:29-39).
+        compile=True replays decode ticks from captured HIP graphs
+        (decode_graph.py) — except in "max-autotune-no-cudagraphs" mode,
+        which by its name asks for no graphs; there is no torch.compile on
+        this path."""
         if not torch.cuda.is_available():
             raise RuntimeError("the engine needs a HIP GPU")
+        if compile_mode not in COMPILE_MODES:
+            raise ValueError(
+                f"unknown compile mode '{compile_mode}'. Valid options: {COMPILE_MODES}"
+            )
         for name, value in (("prefill_chunk_size", prefill_chunk_size),
                             ("max_cache_tokens", max_cache_tokens),
                             ("max_batch_size", max_batch_size)):
@@ -142,9 +156,7 @@ class Engine:
             tokenizer = _local_tokenizer(model_dir)
         self.tokenizer = tokenizer
         if stop_token_ids is None:
-            stop_token_ids = set()
-            if tokenizer is not None and tokenizer.eos_token_id is not None:
-                stop_token_ids.add(int(tokenizer.eos_token_id))
+            stop_token_ids = _stop_token_ids(model_dir, tokenizer)
         self.scheduler = Scheduler(max_batch_size)
         self.prefix_cache = PrefixCache(prefix_cache_max_tokens) if enable_prefix_cache else None
         self.sampler = Sampler(tokenizer, stop_token_ids,
@@ -157,6 +169,10 @@ class Engine:
             num_q_heads=self.model.num_heads,
         )
         self.last_tick = TickStats()
+        self.decode_graphs = (
+            DecodeGraphRunner(self.model, self.paged_cache, self.max_position_embeddings)
+            if compile and compile_mode != "max-autotune-no-cudagraphs" else None
+        )
 
     # ------------------------------------------------------------ requests
     def add_request(self, request: Request) -> None:
@@ -230,6 +246,16 @@ class Engine:
                 if self.prefix_cache is None or not self.prefix_cache.evict_lru():
                     raise
 
+    def _reserve_tick(self, handles, q_lens) -> None:
+        """reserve_tick, evicting cold prefix entries while the pool is full."""
+        while True:
+            try:
+                self.paged_cache.reserve_tick(handles, q_lens)
+                return
+            except MemoryError:
+                if self.prefix_cache is None or not self.prefix_cache.evict_lru():
+                    raise
+
     def _attach(self, request: Request) -> None:
         """Give a new request its pages: a shared prefix (no copy), an
         imported Cache, or none (engine.py:237-243)."""
@@ -269,10 +295,15 @@ class Engine:
             handles.append(r.paged_cache)
             q_lens.append(len(chunk))
             tokens.extend(chunk)
-        paged = self._begin_tick(handles, q_lens)
-        ids = torch.tensor(tokens, dtype=torch.long, device=self.device).unsqueeze(0)
-        with torch.inference_mode():
-            logits, _, _ = self.model(ids, paged_cache=paged)
+        logits = None
+        if self.decode_graphs is not None and all(q == 1 for q in q_lens):
+            self._reserve_tick(handles, q_lens)
+            logits = self.decode_graphs.run(handles, tokens)
+        if logits is None:
+            paged = self._begin_tick(handles, q_lens)
+            ids = torch.tensor(tokens, dtype=torch.long, device=self.device).unsqueeze(0)
+            with torch.inference_mode():
+                logits, _, _ = self.model(ids, paged_cache=paged)
         self.paged_cache.commit_tick(handles, q_lens)
         n_prefill = sum(q for q, r in zip(q_lens, batch) if r.is_prefill)
         self.last_tick = TickStats(len(batch), len(tokens), n_prefill, len(tokens) - n_prefill)
@@ -348,6 +379,27 @@ class Engine:
         while self.generate():
             pass
         return requests[0] if len(requests) == 1 else requests
+
+
+def _stop_token_ids(model_dir: Optional[str], tokenizer) -> set[int]:
+    """End-of-generation ids: the checkpoint's generation_config.json
+    eos_token_id (an id or a list) and the tokenizer's eos id
+    (engine.py:112-129)."""
+    ids: set[int] = set()
+    if model_dir is not None:
+        path = os.path.join(model_dir, "generation_config.json")
+        try:
+            with open(path) as f:
+                eos = json.load(f).get("eos_token_id")
+            if isinstance(eos, int):
+                ids.add(eos)
+            elif eos is not None:
+                ids.update(int(t) for t in eos)
+        except (OSError, ValueError, TypeError):
+            pass  # the tokenizer's id below still applies
+    if tokenizer is not None and tokenizer.eos_token_id is not None:
+        ids.add(int(tokenizer.eos_token_id))
+    return ids
 
 
 def _local_tokenizer(model_dir: str):

@@ -949,6 +949,18 @@ class PagedKVCacheManager:
         """One varlen batch mixing prefill chunks (q_len > 1) and decode
         tokens (q_len == 1); tensors are packed (total_tokens, heads, dim)
         in handle order. Commit with ``commit_tick``."""
+        q_lens = self.reserve_tick(handles, query_lens)
+        return PagedKVBatch(
+            self, q_lens, [h.length for h in handles], [list(h.pages) for h in handles],
+            varlen=True, num_q_heads=self.num_q_heads,
+            tokens_per_split=self.tokens_per_split,
+        )
+
+    def reserve_tick(self, handles: Sequence[PagedCacheHandle],
+                     query_lens: Sequence[int]) -> list[int]:
+        """The checks and reservations of begin_tick without building a
+        batch (for callers that keep their own tick metadata, such as a
+        replayed decode graph); returns the query lengths as ints."""
         self._validate_handles(handles)
         q_lens = [int(q) for q in query_lens]
         if len(q_lens) != len(handles):
@@ -960,11 +972,7 @@ class PagedKVCacheManager:
             raise ValueError(
                 f"page_size must be at least {MIN_KV_PAGE_SIZE} tokens"
             )
-        return PagedKVBatch(
-            self, q_lens, [h.length for h in handles], [list(h.pages) for h in handles],
-            varlen=True, num_q_heads=self.num_q_heads,
-            tokens_per_split=self.tokens_per_split,
-        )
+        return q_lens
 
     def commit_batch(self, handles: Sequence[PagedCacheHandle], query_len: int) -> None:
         """Advance lengths after every layer wrote its states (295-304)."""

@@ -212,3 +212,32 @@ def test_benchmark_reports_prefill_and_decode():
     assert rows[1]["latency_ms_per_step"] > 0
     say(f"  {rows}")
     assert eng.paged_cache.free_page_count == eng.paged_cache.num_pages
+
+
+def test_compiled_engine_replays_decode_graphs_like_eager():
+    """Engine(compile=True) replays decode ticks from captured HIP graphs
+    (decode_graph.py). Over ticks that cross page boundaries, with the
+    batch shrinking as requests finish (3, then 2, then 1 sequences: one
+    capture per batch size), the greedy tokens equal the eager engine's."""
+    say("[engine: decode graphs against eager]")
+    lengths, max_tokens = (120, 250, 40), (12, 30, 8)
+    prompts = [prompt(40 + i, n) for i, n in enumerate(lengths)]
+
+    def run(compiled):
+        eng = make_engine(compile=compiled)
+        reqs = [Request(id=i, prompt_tokens=list(p), max_tokens=m)
+                for i, (p, m) in enumerate(zip(prompts, max_tokens))]
+        for r in reqs:
+            eng.add_request(r)
+        while eng.generate():
+            pass
+        return eng, [r.tokens for r in reqs]
+
+    eager, t_eager = run(False)
+    graphs, t_graph = run(True)
+    assert eager.decode_graphs is None
+    runner = graphs.decode_graphs
+    say(f"  captures {runner.captures}, replays {runner.replays}")
+    assert runner.captures >= 3 and runner.replays >= 25
+    assert t_graph == t_eager
+    assert graphs.paged_cache.free_page_count == graphs.paged_cache.num_pages
