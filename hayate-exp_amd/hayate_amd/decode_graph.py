@@ -103,6 +103,7 @@ class StaticDecodeBatch(PagedKVBatch):
         total = self._off_merge + 4 * B
         self._host = torch.empty(total, dtype=torch.int32, pin_memory=True)
         self._host_np = self._host.numpy()
+        self._copied = None  # event after the last host-to-device copy
         self._dev = torch.zeros(total, dtype=torch.int32, device=self.device)
         d = self._dev
         self.page_table = d[:n_table].view(B, self.max_pages)
@@ -157,6 +158,8 @@ class StaticDecodeBatch(PagedKVBatch):
         if (len(host.decode) > self.record_capacity or host.n_slots > self.slot_capacity
                 or len(host.merge) != B):
             return False
+        if self._copied is not None:
+            self._copied.synchronize()  # the staging buffer is free again
         buf = self._host_np
         table = buf[: B * self.max_pages].reshape(B, self.max_pages)
         table.fill(-1)
@@ -168,10 +171,11 @@ class StaticDecodeBatch(PagedKVBatch):
         dec = host.decode.reshape(-1)
         buf[self._off_dec : self._off_dec + dec.size] = dec
         buf[self._off_merge : self._off_merge + 4 * B] = host.merge.reshape(-1)
-        # the previous tick's copy has completed: the engine reads its
-        # sampled tokens (a synchronisation) before the next refresh
         self._dev.copy_(self._host, non_blocking=True)
+        self._copied = torch.cuda.Event()
+        self._copied.record()
         self.cache_lens.copy_(self.cache_lens_i32, non_blocking=True)
+        self._table_np = table
         self._plan.n_decode = host.n_chunks
         self.cache_lens_host = cache
         self.kv_lens_host = kv
