@@ -36,3 +36,23 @@ def test_checkpoint_name_map_covers_every_parameter():
     assert {id(p) for p in names.values()} == params
     assert "model.layers.1.self_attn.q_norm.weight" in names
     assert len(names) == 3 + 11 * 2
+
+
+def test_stop_ids_from_generation_config_and_tokenizer(tmp_path):
+    """End-of-generation ids (engine.py:112-129 of the reference): the
+    checkpoint's generation_config.json eos id or list, plus the
+    tokenizer's eos id; a missing or broken config leaves the tokenizer's."""
+    import json
+    from types import SimpleNamespace
+
+    from hayate_amd.engine import _stop_token_ids
+
+    tok = SimpleNamespace(eos_token_id=7)
+    (tmp_path / "generation_config.json").write_text(json.dumps({"eos_token_id": [1, 2]}))
+    assert _stop_token_ids(str(tmp_path), tok) == {1, 2, 7}
+    (tmp_path / "generation_config.json").write_text(json.dumps({"eos_token_id": 3}))
+    assert _stop_token_ids(str(tmp_path), None) == {3}
+    (tmp_path / "generation_config.json").write_text("{not json")
+    assert _stop_token_ids(str(tmp_path), tok) == {7}
+    assert _stop_token_ids(None, tok) == {7}
+    assert _stop_token_ids(str(tmp_path / "missing"), None) == set()
