@@ -44,7 +44,7 @@ constexpr double kMergeLaunch = 2.0;
 constexpr double kPartialCost = 0.025;
 constexpr int kDecodeWgPerCu = 1;     // decode workgroups (chunks) per CU
 using hy::kDecodeWaves;                // waves per decode workgroup: partials per piece
-constexpr int64_t kMinChunk = 256;    // smallest decode chunk, in tokens
+constexpr int64_t kMinChunk = 64;     // smallest decode chunk, in tokens (two slices)
 
 // Makespan (in steps) of prefill tiles cut into key ranges of at most
 // `max_steps` steps, dispatched longest first onto `slots` workgroup slots

@@ -14,7 +14,7 @@ then computes the next.
 The planner's decode grid (chunks per kv head) is part of the captured
 launch, so a graph is kept per (batch size, chunk count); the chunk count
 only changes while the batch's total context is under one chunk per CU
-(256 tokens each), and a new count is captured once. The partial-result
+(64 tokens each), and a new count is captured once. The partial-result
 workspace and the work-list buffers are sized for the largest plan of the
 batch size, and the kernels are told that size (their workspace layout
 depends on it), so every tick's plan fits the captured layout.

@@ -147,7 +147,7 @@ int hy_page_scatter(void *pool, int64_t pool_layer_stride,
  *   prefill merge items int32[n][8] =
  *                 {seq, q_begin, q_end, first_slot, num_splits, q_row, 0, 0}.
  * Decode uses one chunk per CU and kv head (num_cus / num_kv_heads chunks,
- * at least 256 tokens each); a chunk also ends after as many pieces as the
+ * at least 64 tokens each); a chunk also ends after as many pieces as the
  * kernel's query table holds. Prefill split lengths are chosen by
  * simulating the longest-first dispatch of the work onto num_cus CUs.
  * counts_out (int32[7]) receives {n_chunks, n_merge, n_decode_slots,

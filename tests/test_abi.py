@@ -217,3 +217,15 @@ def test_entry_points_validate_before_touching_the_device():
     assert lib.hy_paged_prefill_merge(None, 0, 0, 0, None, None, 0, 0, None, 0, 32, 8, 128,
                                       None) == 0
     assert lib.hy_last_error() == b""
+
+
+def test_plan_short_decode_spreads_over_64_token_chunks():
+    """A lone short context still uses many workgroups: chunks of at least
+    64 tokens (two 32-token slices), one per CU and kv head at most."""
+    p = plan([1], [512])
+    chunks, pieces = chunks_and_pieces(p)
+    assert len(chunks) == 512 // 64
+    assert (pieces[:, 2] - pieces[:, 1] == 64).all()
+    p = plan([1] * 4, [4096] * 4)
+    assert len(plan([1] * 4, [4096] * 4).decode) - p.n_chunks >= 4
+    assert p.n_chunks == 256 // 8  # capped at one chunk per CU and kv head
