@@ -7,38 +7,32 @@
 // tile of kPrefillRows / G query tokens of one sequence; with its G query
 // heads that is kPrefillRows (token, head) rows (prefill_shape.h), all
 // reading the same K/V rows (GQA), over the key range [kv_begin, kv_end) of
-// one split. Two 128-row workgroups share a CU, so one's prologue and
-// epilogue overlap the other's main loop.
+// one split. One 512-thread workgroup per CU (96 KiB of LDS).
 //
-// Eight waves of 32 rows, two waves per SIMD: while one wave of a SIMD runs
-// its softmax on the VALU the other one keeps the matrix core busy (a wave
-// cannot overlap its own exp/fma work with its MFMAs). Row r = 32 w + c is
-// token q_begin + r / G, head kv_head * G + r % G, so a wave spans 32 / G
+// Eight waves of 32 rows, two waves per SIMD. Row r = 32 w + c is token
+// q_begin + r / G, head kv_head * G + r % G, so a wave spans 32 / G
 // consecutive tokens and the causal diagonal cuts few of its key blocks.
 //
 // v_mfma_f32_32x32x16_bf16, transposed formulation (lane l, c = l % 32,
 // h = l / 32):
 //   S^T = K Q^T   A = K (32 keys x 16 dims) from LDS (one 16-byte read per
-//                 lane, 272-byte rows: conflict-free); B = Q^T held in
-//                 registers. Lane (c, h) ends with row c's scores for keys
-//                 8 (i / 4) + 4 h + i % 4, i < 16, of the 32-key block.
+//                 lane); B = Q^T held in registers. Lane (c, h) ends with
+//                 row c's scores for keys 8 (i / 4) + 4 h + i % 4, i < 16,
+//                 of the 32-key block.
 //   softmax       per row: the two lanes of a row differ only in h; the
 //                 row max and sum cross halves with v_permlane32_swap.
 //   O^T += V^T P^T  B = P^T: the first (last) eight of the lane's scores
 //                 are row c's probabilities for MFMA k index 8 h + j once k
 //                 stands for key 16 kh + (j < 4 ? 4 h + j : 8 + 4 h + j - 4);
 //                 A = V^T from LDS with ds_read_b64_tr_b16, which hands lane
-//                 r of a 16-lane group four consecutive keys of dim r. One
-//                 read instruction serves 32 lanes (four rows x 64 bytes)
-//                 per LDS cycle; a 320-byte row pitch (80 dwords, 16 mod 64
-//                 banks) puts those four rows on disjoint banks.
-// K/V tiles of KEYS keys are double buffered in LDS and filled by gfx950's
-// 16-byte direct-to-LDS loads (global_load_lds_dwordx4): the next tile's
-// loads go out at the start of a tile and land in the other buffer without
-// passing through registers; one wait and one barrier per tile. A load
-// instruction writes 64 lanes x 16 bytes to consecutive LDS addresses, so
-// the bank-conflict-free layouts are lane permutations instead of padded
-// rows (16-byte units, "chunk" = 8 dims):
+//                 r of a 16-lane group four consecutive keys of dim r.
+// K/V tiles of kTile keys sit in a ring of three LDS stages filled by
+// gfx950's 16-byte direct-to-LDS loads (global_load_lds_dwordx4), two tiles
+// ahead of the one being consumed, without passing through registers; one
+// wait and one barrier per tile. A load instruction writes 64 lanes x 16
+// bytes to consecutive LDS addresses, so the bank-conflict-free layouts are
+// lane permutations instead of padded rows (16-byte units, "chunk" = 8
+// dims):
 //   K: unit(row, chunk) = (row / 16) * 256 + chunk * 16 + row % 16. The
 //      K-operand read (16 lanes = 16 rows, one chunk) touches 16
 //      consecutive units; one load instruction = 16 rows x 4 chunks
@@ -47,11 +41,13 @@
 //      transposing read (32 lanes = 4 rows x 32 dims) touches 16
 //      consecutive units; one load instruction = 4 whole rows.
 // Both give per-lane base addresses with compile-time offsets for every
-// block, dim slice and row group. The softmax rescales lazily: the exponent
-// base of a row only
-// moves when its max grows by more than 2^8, so the accumulators are rarely
-// touched by VALU. Key blocks past the causal limit of every row of a wave
-// are skipped by that wave.
+// block, dim slice and row group. The block loop is software-pipelined: a
+// wave computes block j + 1's scores on the matrix core while its VALU
+// turns block j's scores into probabilities (see the block body below).
+// The softmax rescales lazily: the exponent base of a row only moves when
+// its max grows by more than 2^8, so the accumulators are rarely touched by
+// VALU. Key blocks past the causal limit of every row of a wave are
+// skipped by that wave.
 // Rows at or past kv_end are loaded from the last valid key, so masked
 // scores never meet NaN bits of unwritten rows.
 //
