@@ -241,3 +241,44 @@ def test_compiled_engine_replays_decode_graphs_like_eager():
     assert runner.captures >= 3 and runner.replays >= 25
     assert t_graph == t_eager
     assert graphs.paged_cache.free_page_count == graphs.paged_cache.num_pages
+
+
+def test_compiled_engine_with_prefix_cache_and_admission_matches_eager():
+    """A longer run: 10 requests through a batch limit of 4 (admission
+    over time, so prefill chunks, mixed ticks and decode ticks of sizes 1-4
+    alternate), half of them repeating an earlier prompt (prefix-cache hits
+    whose shared partial page is copied on the first append, inside decode
+    ticks replayed from graphs). Tokens equal the eager engine's; every
+    page comes back."""
+    say("[engine: decode graphs + prefix cache + admission]")
+    base = [prompt(60 + i, n) for i, n in enumerate((300, 130, 520, 90, 260))]
+    prompts = base + [list(p) for p in base]
+    max_tokens = [3 + (i * 7) % 9 for i in range(len(prompts))]
+
+    def run(compiled):
+        eng = make_engine(compile=compiled, enable_prefix_cache=True,
+                          prefix_cache_max_tokens=4096)
+        eng.scheduler.max_batch_size = 4
+        reqs, hits = [], 0
+        for i, (p, m) in enumerate(zip(prompts, max_tokens)):
+            if i == len(base):
+                # the repeats arrive once the originals' prompts are cached
+                while any(r.is_prefill for r in reqs):
+                    eng.generate()
+            r = Request(id=i, prompt_tokens=list(p), max_tokens=m)
+            eng.add_request(r)
+            hits += r.kv_cache is not None
+            reqs.append(r)
+        while eng.generate():
+            pass
+        eng.clear_prefix_cache()
+        assert eng.paged_cache.free_page_count == eng.paged_cache.num_pages
+        return eng, [r.tokens for r in reqs], hits
+
+    _, t_eager, hits_eager = run(False)
+    eng, t_graph, hits_graph = run(True)
+    say(f"  prefix hits {hits_graph}, captures {eng.decode_graphs.captures}, "
+        f"replays {eng.decode_graphs.replays}")
+    assert hits_eager == hits_graph >= 3
+    assert eng.decode_graphs.replays > 0
+    assert t_graph == t_eager
