@@ -1,9 +1,12 @@
 // Paged KV append, fused QK-RMSNorm + RoPE + append, page gather/scatter.
 //
-// Work decomposition: one 16-lane row group per 128-element head row; every
-// lane moves 8 bf16 (16 bytes), so a wave covers four head rows with fully
-// coalesced 256-byte row segments. These kernels are HBM-bound copies; the
-// append kernels keep only the batch's q_start / cache_lens in LDS.
+// Work decomposition: the copies (plain append, gather, scatter) give one
+// 16-lane row group to each 128-element head row, every lane moving 8 bf16
+// (16 bytes), so a wave covers four head rows with fully coalesced 256-byte
+// row segments. The fused norm + rotation + append gives 8 lanes to a row
+// (two 128-byte halves per lane group; see qknorm.h). The plain append
+// keeps the batch's q_start / cache_lens in LDS; the fused one, with one
+// token per wave, reads them with scalar loads.
 //
 // Built with -ffp-contract=off: the norm and rotation must round each fp32
 // product and sum separately, as the reference's chain of elementwise torch
@@ -103,17 +106,37 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 
 // ---------------------------------------------------------------------------
 // Fused q/k RMSNorm + RoPE + K/V append.
-// Grid (token blocks of 16, head groups): blockIdx.y walks the groups of
-// `spb` (<= kMaxSlots) q heads, then those of k heads, then those of v
-// heads; one 16-lane group per token. The token's sequence, position,
-// page, the group's norm weights and the cos/sin row are looked up once
-// per block, and every head's row load is issued before any is processed,
-// so a block keeps spb row loads in flight instead of one dependent chain
-// per head row.
+// Rows in the paired-half layout (qknorm.h): 8 lanes per head row, eight
+// rows side by side in a wave. A wave takes one token and either up to 32
+// of its q heads (four rows per 8-lane group) or up to 8 of its kv heads
+// (the k row normed and rotated into the K pool, the v row copied into the
+// V pool). Grid (token blocks of 4, ceil(Hq / 32) q chunks then
+// ceil(Hkv / 8) kv chunks). The token's sequence, position and page, the
+// norm weights and the cos/sin row are looked up once per wave; the token is
+// uniform over the wave, so the sequence search and the page lookup are
+// scalar loads, which retire on their own counter. Without a per-sequence
+// stride (packed or contiguous batches) a row's address needs only the
+// token index, so the row loads are issued first and stay in flight through
+// the search.
+// The kernel moves each row once and spends about 200 VALU instructions per
+// row and lane group on the exact norm and rotation. Measured on MI355X,
+// four q rows per lane group beat two (8 % slower on a 2,048-token prefill)
+// and one (7 %): the cos/sin row and the weights are then loaded and held
+// for four rows at a time.
 // ---------------------------------------------------------------------------
-constexpr int kMaxSlots = 8;
+constexpr int kTokensPerBlock = 4;  // one token per wave
+constexpr int kQRows = 4;           // q rows per 8-lane group
+constexpr int kQChunk = 8 * kQRows; // q heads per wave
+constexpr int kKvChunk = 8;         // kv heads per wave
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void qknorm_rope_append_kernel(
+__device__ __forceinline__ void load_half_rows(const float *__restrict__ row, int lane,
+                                               float (&lo)[8], float (&hi)[8]) {
+  load_row8(row, lane, lo);
+  load_row8(row + 64, lane, hi);
+}
+
+template <bool kSeqStride>
+__global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const uint16_t *__restrict__ q, int64_t q_ss, int64_t q_st, int64_t q_sh,
     uint16_t *__restrict__ q_out, int64_t qo_ss, int64_t qo_st, int64_t qo_sh,
     const uint16_t *__restrict__ k, int64_t k_ss, int64_t k_st, int64_t k_sh,
@@ -124,81 +147,91 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void q
     uint16_t *__restrict__ v_pool, int64_t pool_hs,
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ cache_lens,
     const int32_t *__restrict__ page_table, int64_t pt_stride, int num_seqs,
-    int total_tokens, int num_q_heads, int num_kv_heads, int page_size, int spb,
+    int total_tokens, int num_q_heads, int num_kv_heads, int page_size,
     int max_positions) {
-  __shared__ int32_t s_qs[kLdsSeqs + 1];
-  __shared__ int32_t s_cl[kLdsSeqs];
-  const SeqMeta meta = stage_seq_meta(s_qs, s_cl, q_start, cache_lens, num_seqs);
-  const int lane = threadIdx.x & 15;
-  const int tok = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
-  if (tok >= total_tokens) return;
-  const int gq = (num_q_heads + spb - 1) / spb;
-  const int gk = (num_kv_heads + spb - 1) / spb;
-  const int gy = blockIdx.y;
-  const int kind = gy < gq ? 0 : gy < gq + gk ? 1 : 2;  // q, k, v heads
-  const int h0 = (kind == 0 ? gy : kind == 1 ? gy - gq : gy - gq - gk) * spb;
-  const int nh = min(spb, (kind == 0 ? num_q_heads : num_kv_heads) - h0);
-  const TokPos tp = meta.locate(tok);
-  const int b = tp.seq;
-  const int pos = tp.pos;
+  const int lane = threadIdx.x & 7;          // position in the row's 8-lane group
+  const int slot = (threadIdx.x >> 3) & 7;   // row group within the wave
+  const int tok = __builtin_amdgcn_readfirstlane(blockIdx.x * kTokensPerBlock + (threadIdx.x >> 6));
+  const int gq = (num_q_heads + kQChunk - 1) / kQChunk;
+  const bool is_q = static_cast<int>(blockIdx.y) < gq;
+  // q: heads h0 + 8 j, j < nrows; kv: k head h0 and v head h0.
+  const int h0 = is_q ? blockIdx.y * kQChunk + slot : (blockIdx.y - gq) * kKvChunk + slot;
+  const int nrows = is_q ? (h0 < num_q_heads ? min(kQRows, (num_q_heads - h0 + 7) / 8) : 0)
+                         : (h0 < num_kv_heads ? 1 : 0);
+  const bool live = tok < total_tokens && nrows > 0;
 
-  // Source rows: base + head * src_sh.
-  const uint16_t *src;
-  int64_t src_sh;
-  if (kind == 0) {
-    src = q + b * q_ss + static_cast<int64_t>(tok) * q_st;
-    src_sh = q_sh;
-  } else if (kind == 1) {
-    src = k + b * k_ss + static_cast<int64_t>(tok) * k_st;
-    src_sh = k_sh;
-  } else {
-    src = v + b * v_ss + static_cast<int64_t>(tok) * v_st;
-    src_sh = v_sh;
-  }
-  src += lane * 8;
-  u32x4 raw[kMaxSlots];
+  // raw[2 j], raw[2 j + 1]: lo and hi halves of q row j; for kv: k then v.
+  u32x4 raw[2 * kQRows];
+  auto issue_loads = [&](int b) {
+    if (is_q) {
+      const uint16_t *src = q + b * q_ss + static_cast<int64_t>(tok) * q_st + h0 * q_sh + lane * 8;
 #pragma unroll
-  for (int j = 0; j < kMaxSlots; ++j)
-    if (j < nh) raw[j] = load16(src + (h0 + j) * src_sh);
-
-  const int64_t p = kind == 0 ? 0 : phys_token(page_table, pt_stride, b, pos, page_size);
-  if (kind == 2) {
-    uint16_t *dst = v_pool + p * kHeadDim + lane * 8;
-#pragma unroll
-    for (int j = 0; j < kMaxSlots; ++j)
-      if (j < nh) store16(dst + (h0 + j) * pool_hs, raw[j]);
-    return;
+      for (int j = 0; j < kQRows; ++j) {
+        if (j < nrows) {
+          raw[2 * j] = load16(src + 8 * j * q_sh);
+          raw[2 * j + 1] = load16(src + 8 * j * q_sh + 64);
+        }
+      }
+    } else {
+      const uint16_t *ks = k + b * k_ss + static_cast<int64_t>(tok) * k_st + h0 * k_sh + lane * 8;
+      const uint16_t *vs = v + b * v_ss + static_cast<int64_t>(tok) * v_st + h0 * v_sh + lane * 8;
+      raw[0] = load16(ks);
+      raw[1] = load16(ks + 64);
+      raw[2] = load16(vs);
+      raw[3] = load16(vs + 64);
+    }
+  };
+  // A whole 8-lane group leaves together, so the group's DPP reads below
+  // only see active lanes.
+  if (!live) return;
+  if (!kSeqStride) issue_loads(0);
+  // Every load is issued before the first use of any: rows, weights, the
+  // token's sequence (scalar), the cos/sin row and the page (scalar).
+  const uint16_t *w = is_q ? q_w : k_w;
+  u32x4 w_lo, w_hi;
+  if (w != nullptr) {
+    w_lo = load16(w + lane * 8);
+    w_hi = load16(w + 64 + lane * 8);
   }
-
-  // Destination rows: the rotated q output, or the K pool.
-  uint16_t *dst = kind == 0 ? q_out + b * qo_ss + static_cast<int64_t>(tok) * qo_st
-                            : k_pool + p * kHeadDim;
-  const int64_t dst_sh = kind == 0 ? qo_sh : pool_hs;
-  dst += lane * 8;
-  const uint16_t *w = kind == 0 ? q_w : k_w;
-  float wf[8];
-  if (w != nullptr) unpack8(load16(w + lane * 8), wf);
-  float cs[8], sn[8];
+  const int b = find_seq(q_start, num_seqs, tok);
+  const int pos = cache_lens[b] + tok - q_start[b];
+  if (kSeqStride) issue_loads(b);
   const bool rot = cos_t != nullptr;
+  float cl[8], ch[8], sl[8], sh[8];
   if (rot) {
     // Positions must be below max_positions (the caller's contract); the
     // clamp only keeps a call that breaks it inside the tables.
     const int64_t off = static_cast<int64_t>(min(pos, max_positions - 1)) * kHeadDim;
-    load_row8(cos_t + off, lane, cs);
-    load_row8(sin_t + off, lane, sn);
-    const float sgn = lane < 8 ? -1.0f : 1.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sn[j] *= sgn;
+    load_half_rows(cos_t + off, lane, cl, ch);
+    load_half_rows(sin_t + off, lane, sl, sh);
   }
-#pragma unroll
-  for (int j = 0; j < kMaxSlots; ++j) {
-    if (j >= nh) break;
-    float x[8];
-    unpack8(raw[j], x);
-    if (w != nullptr) rms_norm8(x, wf, eps);
-    if (rot) rope8_signed(x, cs, sn);
-    store16(dst + (h0 + j) * dst_sh, pack8_rne(x));
+  const int64_t p = is_q ? 0 : phys_token(page_table, pt_stride, b, pos, page_size);
+
+  float wl[8], wh[8];
+  if (w != nullptr) {
+    unpack8(w_lo, wl);
+    unpack8(w_hi, wh);
   }
+  auto finish_row = [&](u32x4 lo, u32x4 hi, uint16_t *dst) {
+    float xl[8], xh[8];
+    unpack8(lo, xl);
+    unpack8(hi, xh);
+    if (w != nullptr) rms_norm16(xl, xh, wl, wh, eps);
+    if (rot) rope16(xl, xh, cl, ch, sl, sh);
+    store16(dst, pack8_rne(xl));
+    store16(dst + 64, pack8_rne(xh));
+  };
+  if (is_q) {
+    uint16_t *dst = q_out + b * qo_ss + static_cast<int64_t>(tok) * qo_st + h0 * qo_sh + lane * 8;
+#pragma unroll
+    for (int j = 0; j < kQRows; ++j)
+      if (j < nrows) finish_row(raw[2 * j], raw[2 * j + 1], dst + 8 * j * qo_sh);
+    return;
+  }
+  const int64_t row = h0 * pool_hs + p * kHeadDim + lane * 8;
+  store16(v_pool + row, raw[2]);
+  store16(v_pool + row + 64, raw[3]);
+  finish_row(raw[0], raw[1], k_pool + row);
 }
 
 // ---------------------------------------------------------------------------
@@ -356,18 +389,16 @@ extern "C" int hy_qknorm_rope_append(
   if (total_tokens == 0) return HY_OK;
   HY_REQUIRE(num_q_heads + 2 * num_kv_heads <= 65535, "too many heads (%d q, %d kv)",
              num_q_heads, num_kv_heads);
-  // Heads per block: as many as keep about four blocks per CU, so that
-  // short ticks still spread over the chip.
-  const int64_t token_blocks = hy::grid_for_rows(total_tokens);
-  auto groups = [&](int spb) {
-    return (num_q_heads + spb - 1) / spb + 2 * ((num_kv_heads + spb - 1) / spb);
-  };
-  int spb = hy::kMaxSlots;
-  while (spb > 1 && token_blocks * groups(spb) < 1024) spb /= 2;
+  const int gq = (num_q_heads + hy::kQChunk - 1) / hy::kQChunk;
+  const int gkv = (num_kv_heads + hy::kKvChunk - 1) / hy::kKvChunk;
+  // Row addresses that need no sequence index let the kernel load rows
+  // before it searches for the token's sequence.
+  const bool seq_stride = q_stride_seq || qo_stride_seq || k_stride_seq || v_stride_seq;
+  auto kernel = seq_stride ? hy::qknorm_rope_append_kernel<true>
+                           : hy::qknorm_rope_append_kernel<false>;
   hipLaunchKernelGGL(
-      hy::qknorm_rope_append_kernel,
-      dim3(token_blocks, groups(spb)), dim3(256),
-      0, static_cast<hipStream_t>(stream), static_cast<const uint16_t *>(q),
+      kernel, dim3((total_tokens + hy::kTokensPerBlock - 1) / hy::kTokensPerBlock, gq + gkv),
+      dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const uint16_t *>(q),
       q_stride_seq, q_stride_tok, q_stride_head, static_cast<uint16_t *>(q_out),
       qo_stride_seq, qo_stride_tok, qo_stride_head,
       static_cast<const uint16_t *>(k), k_stride_seq, k_stride_tok,
@@ -377,7 +408,7 @@ extern "C" int hy_qknorm_rope_append(
       static_cast<const uint16_t *>(k_norm_weight), eps, cos_table, sin_table,
       static_cast<uint16_t *>(k_pool), static_cast<uint16_t *>(v_pool),
       pool_head_stride, q_start, cache_lens, page_table, page_table_stride,
-      num_seqs, total_tokens, num_q_heads, num_kv_heads, page_size, spb, max_positions);
+      num_seqs, total_tokens, num_q_heads, num_kv_heads, page_size, max_positions);
   return hy::launch_status("hy_qknorm_rope_append");
 }
 

@@ -64,15 +64,20 @@ __device__ __forceinline__ double row16_sum_f64(double x) {
   return x;
 }
 
+// rsqrt(mean + eps) of a head row from its fp64 sum of squares: the mean
+// rounded to fp32, then sqrt and reciprocal each correctly rounded to fp32.
+__device__ __forceinline__ float rms_rstd(double ss, float eps) {
+  const float mean = static_cast<float>(ss) * (1.0f / kHeadDim);
+  const float root = static_cast<float>(sqrt(static_cast<double>(mean + eps)));
+  return static_cast<float>(1.0 / static_cast<double>(root));
+}
+
 // wf: the 8 weights of this lane's features, already widened to fp32.
 __device__ __forceinline__ void rms_norm8(float (&x)[8], const float (&wf)[8], float eps) {
   double ss = 0.0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ss += static_cast<double>(x[j] * x[j]);
-  ss = row16_sum_f64(ss);
-  const float mean = static_cast<float>(ss) * (1.0f / kHeadDim);
-  const float root = static_cast<float>(sqrt(static_cast<double>(mean + eps)));
-  const float rstd = static_cast<float>(1.0 / static_cast<double>(root));
+  const float rstd = rms_rstd(row16_sum_f64(ss), eps);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t w = pack_bf16x2_rne((x[2 * j] * rstd) * wf[2 * j],
@@ -133,6 +138,78 @@ __device__ __forceinline__ void rope8(float (&x)[8],
 #pragma unroll
   for (int j = 0; j < 8; ++j) s[j] *= sgn;
   rope8_signed(x, c, s);
+}
+
+// ---------------------------------------------------------------------------
+// Paired-half row layout: a head row is held by an aligned group of 8 lanes,
+// lane l of the group holding features [8l, 8l + 8) ("lo") and
+// [64 + 8l, 64 + 8l + 8) ("hi"). rotate_half pairs feature i with i + 64,
+// so the rotation stays inside a lane, and the norm's row reduction spans 8
+// lanes.
+// ---------------------------------------------------------------------------
+template <int Ctrl>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(x));
+  const uint64_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(u)), Ctrl, 0xf, 0xf, false));
+  const uint64_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_mov_dpp(static_cast<int>(static_cast<uint32_t>(u >> 32)), Ctrl, 0xf, 0xf, false));
+  return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
+}
+
+// Sum over the 8 lanes of an aligned group, in every lane: lane ^ 1 and
+// lane ^ 2 (quad permutations), then lane i with 7 - i (half-row mirror).
+// Each step adds two operands that every lane of the pair holds in swapped
+// order, so all 8 lanes end with the same bits.
+__device__ __forceinline__ double group8_sum_f64(double x) {
+  x += dpp_f64<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x += dpp_f64<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x += dpp_f64<0x141>(x);  // row_half_mirror
+  return x;
+}
+
+// RMSNorm of a row in the paired-half layout (same arithmetic as
+// rms_norm8): squares of bf16 values are exact in fp64, so fma(x, x, ss)
+// adds the exact square.
+__device__ __forceinline__ void rms_norm16(float (&xl)[8], float (&xh)[8], const float (&wl)[8],
+                                           const float (&wh)[8], float eps) {
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const double a = static_cast<double>(xl[j]);
+    const double b = static_cast<double>(xh[j]);
+    ss = __builtin_fma(a, a, ss);
+    ss = __builtin_fma(b, b, ss);
+  }
+  const float rstd = rms_rstd(group8_sum_f64(ss), eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t a = pack_bf16x2_rne((xl[2 * j] * rstd) * wl[2 * j],
+                                       (xl[2 * j + 1] * rstd) * wl[2 * j + 1]);
+    const uint32_t b = pack_bf16x2_rne((xh[2 * j] * rstd) * wh[2 * j],
+                                       (xh[2 * j + 1] * rstd) * wh[2 * j + 1]);
+    xl[2 * j] = bf16_lo(a);
+    xl[2 * j + 1] = bf16_hi(a);
+    xh[2 * j] = bf16_lo(b);
+    xh[2 * j + 1] = bf16_hi(b);
+  }
+}
+
+// y = x * cos + rotate_half(x) * sin in the paired-half layout:
+// lo: x_lo * c_lo + (-x_hi) * s_lo, rounded as x_lo * c_lo - x_hi * s_lo
+// (negation is exact); hi: x_hi * c_hi + x_lo * s_hi.
+__device__ __forceinline__ void rope16(float (&xl)[8], float (&xh)[8], const float (&cl)[8],
+                                       const float (&ch)[8], const float (&sl)[8],
+                                       const float (&sh)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float a = xl[j] * cl[j];
+    const float b = xh[j] * sl[j];
+    const float c = xh[j] * ch[j];
+    const float d = xl[j] * sh[j];
+    xl[j] = a - b;
+    xh[j] = c + d;
+  }
 }
 
 }  // namespace hy
