@@ -433,6 +433,12 @@ void prefill_kernel(
     if (masked) mask(s_cur, kv_begin + 32 * j);  // blocks on the diagonal
     read_v(j, 0);
     __builtin_amdgcn_sched_barrier(0);
+    // The two waves of a SIMD take turns: the one in this region (next
+    // block's QK^T interleaved with this block's probabilities, the chain
+    // that gates its next block) wins issue over the other wave's P V, K
+    // reads and barrier wait. Measured on prefill_4x512: 4 % less kernel
+    // time than without the priority (and than a priority on P V).
+    __builtin_amdgcn_s_setprio(1);
     s_nxt = qk();
     read_v(j, 1);
     probs(s_cur, pop0, pop1, psum, mx);
@@ -446,6 +452,7 @@ void prefill_kernel(
     // this straight-line region instead of sinking them past the rebase test
     __asm__ volatile("" ::"v"(psum), "v"(pop0), "v"(pop1));
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     rebase(s_cur, mx, pop0, pop1, psum);
     s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_nxt, 0, 0, 0);
     read_k(j + 2);
