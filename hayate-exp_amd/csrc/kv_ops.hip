@@ -4,9 +4,8 @@
 // 16-lane row group to each 128-element head row, every lane moving 8 bf16
 // (16 bytes), so a wave covers four head rows with fully coalesced 256-byte
 // row segments. The fused norm + rotation + append gives 8 lanes to a row
-// (two 128-byte halves per lane group; see qknorm.h). The plain append
-// keeps the batch's q_start / cache_lens in LDS; the fused one, with one
-// token per wave, reads them with scalar loads.
+// (two 128-byte halves per lane group; see qknorm.h). Both appends take one
+// token per wave and read its sequence, position and page with scalar loads.
 //
 // Built with -ffp-contract=off: the norm and rotation must round each fp32
 // product and sum separately, as the reference's chain of elementwise torch
@@ -22,47 +21,8 @@ namespace hy {
 
 namespace {
 
-constexpr int kRowsPerBlock = 16;  // 256 threads = 16 head rows
-constexpr int kLdsSeqs = 1024;     // batches up to this size stage their metadata in LDS
-
-// Per-block copy of q_start and cache_lens in LDS: the token -> sequence
-// search and the position lookup then cost LDS reads instead of a chain of
-// dependent global loads (one per binary-search step). Larger batches read
-// global memory directly.
-struct TokPos {
-  int seq, pos;  // sequence of the token and its position in that sequence
-};
-
-struct SeqMeta {
-  const int32_t *s_qs, *s_cl;  // LDS copies (valid when staged)
-  const int32_t *q_start, *cache_lens;
-  int num_seqs;
-  bool staged;
-
-  __device__ __forceinline__ TokPos locate(int tok) const {
-    if (staged) {
-      const int b = find_seq(s_qs, num_seqs, tok);
-      return {b, s_cl[b] + tok - s_qs[b]};
-    }
-    const int b = find_seq(q_start, num_seqs, tok);
-    return {b, cache_lens[b] + tok - q_start[b]};
-  }
-};
-
-__device__ __forceinline__ SeqMeta stage_seq_meta(int32_t *s_qs, int32_t *s_cl,
-                                                 const int32_t *__restrict__ q_start,
-                                                 const int32_t *__restrict__ cache_lens,
-                                                 int num_seqs) {
-  const bool staged = num_seqs <= kLdsSeqs;
-  if (staged) {
-    for (int j = threadIdx.x; j <= num_seqs; j += blockDim.x) {
-      s_qs[j] = q_start[j];
-      if (j < num_seqs) s_cl[j] = cache_lens[j];
-    }
-    __syncthreads();
-  }
-  return {s_qs, s_cl, q_start, cache_lens, num_seqs, staged};
-}
+constexpr int kRowsPerBlock = 16;   // copies: 256 threads = 16 head rows
+constexpr int kTokensPerBlock = 4;  // appends: one token per wave
 
 // Physical token index of logical position t of sequence b.
 __device__ __forceinline__ int64_t phys_token(const int32_t *__restrict__ pt,
@@ -74,9 +34,12 @@ __device__ __forceinline__ int64_t phys_token(const int32_t *__restrict__ pt,
 
 // ---------------------------------------------------------------------------
 // Plain append: pool[h, phys(b, c_b + i)] = src[b, i, h]  (K and V).
-// Grid (token blocks of 16, 2 Hkv): blockIdx.y < Hkv is K head blockIdx.y,
-// the rest V heads; one 16-lane group per token.
+// One token per wave and 8 kv heads per grid row (blockIdx.y): the wave's 16
+// rows (8 K, 8 V) go in four 16-lane row loads per lane. The token is
+// wave-uniform, so its sequence and page are scalar loads; without a
+// per-sequence stride the row loads are issued before them.
 // ---------------------------------------------------------------------------
+template <bool kSeqStride>
 __global__ __launch_bounds__(256) void kv_append_kernel(
     uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool,
     int64_t pool_hs, const uint16_t *__restrict__ k, int64_t k_ss,
@@ -85,23 +48,35 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     const int32_t *__restrict__ cache_lens,
     const int32_t *__restrict__ page_table, int64_t pt_stride, int num_seqs,
     int total_tokens, int num_kv_heads, int page_size) {
-  __shared__ int32_t s_qs[kLdsSeqs + 1];
-  __shared__ int32_t s_cl[kLdsSeqs];
-  const SeqMeta meta = stage_seq_meta(s_qs, s_cl, q_start, cache_lens, num_seqs);
-  const int lane = threadIdx.x & 15;
-  const int tok = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 4);
+  const int tok = __builtin_amdgcn_readfirstlane(blockIdx.x * kTokensPerBlock + (threadIdx.x >> 6));
   if (tok >= total_tokens) return;
-  const bool is_v = static_cast<int>(blockIdx.y) >= num_kv_heads;
-  const int h = is_v ? blockIdx.y - num_kv_heads : blockIdx.y;
-  const TokPos tp = meta.locate(tok);
-  const int b = tp.seq;
-  const int pos = tp.pos;
+  const int lane = threadIdx.x & 15;
+  const int grp = (threadIdx.x >> 4) & 3;  // row within one four-row load
+  // Row 4 j + grp of the wave: K head h0 + r for r < 8, else V head h0 + r - 8.
+  const int h0 = blockIdx.y * 8;
+  u32x4 raw[4];
+  auto issue_loads = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 4 * j + grp;
+      const int h = h0 + (r & 7);
+      if (h >= num_kv_heads) continue;
+      raw[j] = load16(r < 8 ? k + b * k_ss + static_cast<int64_t>(tok) * k_st + h * k_sh + lane * 8
+                            : v + b * v_ss + static_cast<int64_t>(tok) * v_st + h * v_sh + lane * 8);
+    }
+  };
+  if (!kSeqStride) issue_loads(0);
+  const int b = find_seq(q_start, num_seqs, tok);
+  const int pos = cache_lens[b] + tok - q_start[b];
+  if (kSeqStride) issue_loads(b);
   const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);
-
-  const uint16_t *src = is_v ? v + b * v_ss + static_cast<int64_t>(tok) * v_st + h * v_sh
-                             : k + b * k_ss + static_cast<int64_t>(tok) * k_st + h * k_sh;
-  uint16_t *dst = (is_v ? v_pool : k_pool) + h * pool_hs + p * kHeadDim;
-  store16(dst + lane * 8, load16(src + lane * 8));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * j + grp;
+    const int h = h0 + (r & 7);
+    if (h >= num_kv_heads) continue;
+    store16((r < 8 ? k_pool : v_pool) + h * pool_hs + p * kHeadDim + lane * 8, raw[j]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -124,7 +99,6 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 // and one (7 %): the cos/sin row and the weights are then loaded and held
 // for four rows at a time.
 // ---------------------------------------------------------------------------
-constexpr int kTokensPerBlock = 4;  // one token per wave
 constexpr int kQRows = 4;           // q rows per 8-lane group
 constexpr int kQChunk = 8 * kQRows; // q heads per wave
 constexpr int kKvChunk = 8;         // kv heads per wave
@@ -346,9 +320,12 @@ extern "C" int hy_kv_append(void *k_pool, void *v_pool,
   HY_REQUIRE(k_pool && v_pool && k && v && q_start && cache_lens && page_table,
              "hy_kv_append: null pointer argument");
   if (total_tokens == 0) return HY_OK;
-  HY_REQUIRE(2 * num_kv_heads <= 65535, "num_kv_heads (%d) too large", num_kv_heads);
-  hipLaunchKernelGGL(hy::kv_append_kernel,
-                     dim3(hy::grid_for_rows(total_tokens), 2 * num_kv_heads),
+  HY_REQUIRE((num_kv_heads + 7) / 8 <= 65535, "num_kv_heads (%d) too large", num_kv_heads);
+  const bool seq_stride = k_stride_seq || v_stride_seq;
+  auto kernel = seq_stride ? hy::kv_append_kernel<true> : hy::kv_append_kernel<false>;
+  hipLaunchKernelGGL(kernel,
+                     dim3((total_tokens + hy::kTokensPerBlock - 1) / hy::kTokensPerBlock,
+                          (num_kv_heads + 7) / 8),
                      dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<uint16_t *>(k_pool),
                      static_cast<uint16_t *>(v_pool), pool_head_stride,

@@ -11,7 +11,7 @@ path and check them against the oracle:
 * the module at T == 1 on a uniform batch (the fused decode_layer on
   (B, 1, H, D) strides) at the batch-32 decode lengths;
 * write_layer + attend_layer at T == 1 on the uniform (B, H, 1, D) layout
-  (the plain decode kernel);
+  (the plain decode kernel), and write_layer on a packed varlen tick;
 * the module on a uniform 512-token prefill;
 * the module's varlen branch (one packed begin_tick mixing prefill chunks
   and decode tokens, and an all-decode varlen tick);
@@ -188,6 +188,35 @@ def test_uniform_write_and_attend_at_t1():
                                pools.v[0], page_lists, cache_lens, [1] * 32, P)
     assert_attention_close(bits(out.transpose(1, 2)).reshape(32, HQ, D), expect,
                            "uniform attend T=1")
+
+
+def test_write_layer_packed_varlen_tick():
+    """write_layer on a packed (N, Hkv, D) varlen tick, whose rows are
+    addressed by token index alone (the append loads them before it looks
+    the token's sequence up), with 8 kv heads and with 12, whose second
+    8-head group is partly empty: pools bit-exact against the oracle."""
+    cache_lens = [0, 130, 511, 1000, 77]
+    q_lens = [300, 1, 1, 64, 129]
+    for hkv in (HKV, 12):
+        say(f"[write_layer packed varlen tick, {hkv} kv heads]")
+        pool = (sum(math.ceil((c + q) / P) for c, q in zip(cache_lens, q_lens)) + 8) * P
+        m = PagedKVCacheManager(1, hkv, D, pool, P, len(cache_lens), torch.bfloat16, DEV,
+                                num_q_heads=hkv)
+        g = torch.Generator(device=DEV).manual_seed(20)
+        m.k_cache.normal_(generator=g)
+        m.v_cache.normal_(generator=g)
+        handles = place(m, cache_lens, 21)
+        pools = OraclePools(m)
+        batch = m.begin_tick(handles, q_lens)
+        page_lists = [list(h.pages) for h in handles]
+        n = sum(q_lens)
+        gh = torch.Generator().manual_seed(22)
+        k = torch.randn(n, hkv, D, generator=gh).to(torch.bfloat16).to(DEV)
+        v = torch.randn(n, hkv, D, generator=gh).to(torch.bfloat16).to(DEV)
+        batch.write_layer(0, k, v)
+        torch.cuda.synchronize()
+        R.kv_append(pools.k[0], pools.v[0], bits(k), bits(v), page_lists, cache_lens, q_lens, P)
+        pools.check(m, f"packed write_layer, {hkv} kv heads")
 
 
 def test_module_uniform_prefill_512():

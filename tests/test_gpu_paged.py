@@ -217,10 +217,10 @@ def test_page_size_256():
     _ragged([300, 0, 1000], [1, 70, 1], page_size=256)
 
 
-def test_more_sequences_than_the_staged_metadata():
-    """1,100 sequences: past the 1,024 the append kernels stage in LDS, so
-    they look sequences up in global memory; decode chunks hold many
-    pieces. Plain and fused decode, then a mixed tick with prefill chunks."""
+def test_more_than_a_thousand_sequences():
+    """1,100 sequences: a ten-step sequence search per token in the append
+    kernels, decode chunks that hold many pieces. Plain and fused decode,
+    then a mixed tick with prefill chunks."""
     n = 1100
     cache_lens = [(7 * i) % 300 for i in range(n)]
     _ragged(cache_lens, [1] * n, pool_tokens=(n + 4) * 384)
