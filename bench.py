@@ -392,8 +392,9 @@ def cpu_baseline(names, runs=3):
         "kind": "port",
         "sample": ("the reference's CPU path restated (paged write + torch.compile'd "
                    "flex_attention over the physical-page BlockMask, oracle/flex_ref.py), "
-                   f"decode_b32 at full size, median of {runs} calls after one warm-up "
-                   "call that includes the compile; per-workload rows in 'configs'"),
+                   f"every listed workload at full size (value: decode_b32), median of "
+                   f"{runs} calls after one warm-up call that includes the compile; "
+                   "per-workload rows in 'configs'"),
         "cpu_model": model,
         "logical_cpus": logical,
         "threads": threads,
@@ -428,8 +429,10 @@ def main():
     ap.add_argument("--split", type=int, default=0, help="decode tokens per split (0 = auto)")
     ap.add_argument("--only", default="", help="comma-separated workloads (default: all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-configs", default="decode_b1,decode_b32",
-                    help="workloads timed on the CPU path (comma-separated, or 'all')")
+    ap.add_argument("--cpu-configs", default="all",
+                    help="workloads timed on the CPU path (comma-separated, or 'all'); all "
+                         "five at full size take about 30 s of host time, most of it the "
+                         "first compile")
     ap.add_argument("--no-engine", action="store_true", help="skip the 36-layer engine ticks")
     args = ap.parse_args()
 
