@@ -24,8 +24,9 @@ from oracle import paged_ref as R
 pytestmark = pytest.mark.gpu
 
 if torch.cuda.is_available():
-    from hayate_amd import Cache, PagedKVCacheManager
+    from hayate_amd import Cache, PagedKVBatch, PagedKVCacheManager
     from hayate_amd.attention import GroupedQueryAttention
+    from hayate_amd.constants import MIN_KV_PAGE_SIZE
     from hayate_amd.rope import compute_rope_params
     from hayate_amd.workloads import ORDER, make_workload
 else:  # collected on CPU only to be deselected
@@ -175,7 +176,14 @@ def _ragged(cache_lens, q_lens, page_size=128, pool_tokens=32768, seed=0):
     k = torch.randn(n_tok, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
     v = torch.randn(n_tok, hkv, d, generator=g).to(torch.bfloat16).to(DEV)
     pre_k, pre_v = layer_bits(m)
-    batch = m.begin_tick(handles, q_lens)
+    if page_size >= MIN_KV_PAGE_SIZE:
+        batch = m.begin_tick(handles, q_lens)
+    else:
+        # begin_tick keeps the reference's smallest page (128 tokens); the
+        # C ABI takes any power of two >= 32, so the batch is built directly
+        # over the pages the handles already hold
+        batch = PagedKVBatch(m, list(q_lens), list(cache_lens), [list(h.pages) for h in handles],
+                             varlen=True, num_q_heads=hq, tokens_per_split=m.tokens_per_split)
     batch.write_layer(0, k, v)
     out = batch.attend_layer(q, 0)
     torch.cuda.synchronize()
@@ -215,6 +223,17 @@ def test_prefill_deep_prefix_splits():
 
 def test_page_size_256():
     _ragged([300, 0, 1000], [1, 70, 1], page_size=256)
+
+
+@pytest.mark.parametrize("page_size", [32, 64])
+def test_small_pages_through_the_c_abi(page_size):
+    """Pages of 32 and 64 tokens (the kernels' smallest: a 32-token slice or
+    key block must lie in one page): decode contexts around slice and page
+    edges, unaligned prefill chunks, and a chunk over a prefix deep enough
+    for the planner to split its key range."""
+    ctx = [1, 31, 32, 33, 63, 64, 65, 129, 1000]
+    _ragged([c - 1 for c in ctx] + [0, 95, 6000], [1] * len(ctx) + [61, 130, 300],
+            page_size=page_size, pool_tokens=16384)
 
 
 def test_more_than_a_thousand_sequences():
