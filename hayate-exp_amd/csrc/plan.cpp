@@ -36,10 +36,15 @@ constexpr int kSlice = 32;        // decode kernel's token slice
 using hy::kPrefillRows;                          // rows of a prefill workgroup
 constexpr int kPrefillKeys = hy::kPrefillTileKeys;  // keys per prefill step
 // Prefill cost model, in units of one step (64 keys) of one workgroup,
-// measured on MI355X: a workgroup's fixed cost (Q load, first tile,
-// epilogue) is about two steps; the merge launch about two steps; one
-// split partial (write + read of its rows of fp32 O) a fortieth of a step.
-constexpr double kPrefillFixed = 2.0;
+// measured on MI355X from per-workgroup start/end stamps (s_memrealtime) on
+// the 4 x 512 chunked prefill and the mixed tick: a workgroup takes 5.35 us
+// + 1.86 us per step, so its fixed cost (Q load, first tiles, epilogue) is
+// about 2.9 steps; a workgroup that follows another on the same CU starts
+// 6.4 us (3.4 steps) after the previous one's last step; the merge launch
+// costs about two steps and one split partial (write + read of its rows of
+// fp32 O) a fortieth of a step.
+constexpr double kPrefillFixed = 2.9;
+constexpr double kPrefillGap = 3.4;
 constexpr double kMergeLaunch = 2.0;
 constexpr double kPartialCost = 0.025;
 constexpr int kDecodeWgPerCu = 1;     // decode workgroups (chunks) per CU
@@ -67,7 +72,7 @@ double prefill_cost(const std::vector<int64_t> &tile_steps, int64_t max_steps, i
   double makespan = 0.0;
   for (double c : costs)
     for (int h = 0; h < num_kv_heads; ++h) {
-      const double t = free_at.top() + c;
+      const double t = free_at.top() + c + (free_at.top() > 0.0 ? kPrefillGap : 0.0);
       free_at.pop();
       free_at.push(t);
       makespan = std::max(makespan, t);
