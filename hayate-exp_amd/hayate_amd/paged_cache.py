@@ -397,6 +397,8 @@ class PagedKVBatch:
         qos = self._layout(q_out, "bthd")
         ks = self._layout(k, "bthd")
         vs = self._layout(v, "bthd")
+        if (cos is None) != (sin is None):
+            raise ValueError("cos and sin rope tables go together (both or neither)")
         if cos is not None:
             if cos.dtype != torch.float32 or sin.dtype != torch.float32:
                 raise TypeError("rope tables must be float32")
