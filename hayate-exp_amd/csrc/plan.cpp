@@ -12,6 +12,7 @@
 // dispatch says so, and work is ordered longest first so the short items
 // fill in behind the long ones.
 
+#include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -51,34 +52,87 @@ constexpr int kDecodeWgPerCu = 1;     // decode workgroups (chunks) per CU
 using hy::kDecodeWaves;                // waves per decode workgroup: partials per piece
 constexpr int64_t kMinChunk = 64;     // smallest decode chunk, in tokens (two slices)
 
-// Makespan (in steps) of prefill tiles cut into key ranges of at most
-// `max_steps` steps, dispatched longest first onto `slots` workgroup slots
-// (each kv head a separate workgroup), plus the merge launch and the merge
-// traffic of the partials they create.
-double prefill_cost(const std::vector<int64_t> &tile_steps, int64_t max_steps, int num_kv_heads,
-                    int64_t slots) {
-  std::vector<double> costs;
-  int64_t partials = 0;
-  for (int64_t st : tile_steps) {
-    const int64_t n = (st + max_steps - 1) / max_steps;
-    const int64_t per = (st + n - 1) / n;
-    for (int64_t a = 0; a < st; a += per)
-      costs.push_back(static_cast<double>(std::min(per, st - a)) + kPrefillFixed);
-    if (n > 1) partials += n;
+// How a prefill tile of `steps` key steps is cut into key ranges (parts).
+// Even: the fewest parts of at most `len` steps, of equal length (+-1).
+// Capped: parts of exactly `len` steps from the start and the remainder as a
+// last, shorter part when it has at least `min_rest` steps (a short part
+// fills the second slot of a CU whose first workgroup was short); a smaller
+// remainder is spread over the full parts instead.
+struct SplitRule {
+  bool capped;
+  int64_t len, min_rest;
+};
+
+void split_tile(int64_t steps, const SplitRule &r, std::vector<int64_t> &parts) {
+  parts.clear();
+  if (steps <= r.len) {
+    parts.push_back(steps);
+    return;
   }
-  std::sort(costs.begin(), costs.end(), std::greater<double>());
-  std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
-  for (int64_t i = 0; i < slots; ++i) free_at.push(0.0);
-  double makespan = 0.0;
-  for (double c : costs)
-    for (int h = 0; h < num_kv_heads; ++h) {
-      const double t = free_at.top() + c + (free_at.top() > 0.0 ? kPrefillGap : 0.0);
-      free_at.pop();
-      free_at.push(t);
-      makespan = std::max(makespan, t);
+  int64_t n = (steps + r.len - 1) / r.len;
+  if (r.capped) {
+    const int64_t full = steps / r.len;
+    const int64_t rest = steps - full * r.len;
+    if (rest == 0 || rest >= r.min_rest) {
+      for (int64_t i = 0; i < full; ++i) parts.push_back(r.len);
+      if (rest) parts.push_back(rest);
+      return;
     }
-  return makespan + (partials ? kMergeLaunch : 0.0) + kPartialCost * partials * num_kv_heads;
+    n = full;
+  }
+  for (int64_t i = 0; i < n; ++i) parts.push_back(steps / n + (i < steps % n ? 1 : 0));
 }
+
+// Makespan (in steps) of prefill tiles cut by `rule`, dispatched longest
+// first onto `slots` workgroup slots (each kv head a separate workgroup),
+// plus the merge launch and the merge traffic of the partials they create.
+// With the slots a multiple of the kv heads, the copies of an item for the
+// kv heads go to equally loaded slots, so one head on slots / heads slots
+// gives the same makespan. The buffers are kept between calls, and a run
+// stops as soon as it cannot end below `bound` (its value is then >= bound).
+struct PrefillSim {
+  std::vector<double> costs, free_at;
+  std::vector<int64_t> parts;
+
+  double cost(const std::vector<int64_t> &tile_steps, const SplitRule &rule, int num_kv_heads,
+              int64_t slots, double bound) {
+    costs.clear();
+    int64_t partials = 0;
+    double longest = 0.0, total = 0.0;
+    for (int64_t st : tile_steps) {
+      split_tile(st, rule, parts);
+      for (int64_t p : parts) {
+        costs.push_back(static_cast<double>(p) + kPrefillFixed);
+        longest = std::max(longest, costs.back());
+        total += costs.back();
+      }
+      if (parts.size() > 1) partials += static_cast<int64_t>(parts.size());
+    }
+    const double extra =
+        (partials ? kMergeLaunch : 0.0) + kPartialCost * static_cast<double>(partials * num_kv_heads);
+    int copies = num_kv_heads;
+    if (slots % num_kv_heads == 0) {
+      slots /= num_kv_heads;
+      copies = 1;
+    }
+    // Lower bounds first: the longest part, and all the work spread evenly.
+    const double floor = std::max(longest, total * copies / static_cast<double>(slots)) + extra;
+    if (costs.empty() || floor >= bound) return floor;
+    std::sort(costs.begin(), costs.end(), std::greater<double>());
+    free_at.assign(static_cast<size_t>(slots), 0.0);  // a min-heap (all equal)
+    double makespan = 0.0;
+    for (double c : costs)
+      for (int h = 0; h < copies; ++h) {
+        std::pop_heap(free_at.begin(), free_at.end(), std::greater<double>());
+        double &slot = free_at.back();
+        slot += c + (slot > 0.0 ? kPrefillGap : 0.0);
+        makespan = std::max(makespan, slot);
+        std::push_heap(free_at.begin(), free_at.end(), std::greater<double>());
+        if (makespan + extra >= bound) return makespan + extra;
+      }
+    return makespan + extra;
+  }
+};
 
 }  // namespace
 
@@ -246,8 +300,8 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
   }
 
   // Prefill: query tiles of kPrefillRows / G tokens; the key range of a tile is
-  // [0, cache_len + q_end). The longest tiles are split into key ranges of
-  // at most max_steps 64-key steps when that shortens the simulated run.
+  // [0, cache_len + q_end). The longest tiles are split into key ranges by
+  // the split rule whose simulated run is shortest.
   struct Tile {
     int32_t seq, q0, q1, kv_end;
     int64_t steps;
@@ -266,20 +320,27 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
       max_tile_steps = std::max(max_tile_steps, st);
     }
   }
-  int64_t max_steps = std::max<int64_t>(max_tile_steps, 1);
+  SplitRule rule{false, std::max<int64_t>(max_tile_steps, 1), 0};
   if (!tiles.empty()) {
     std::vector<int64_t> tile_steps;
     for (const Tile &t : tiles) tile_steps.push_back(t.steps);
     const int64_t slots = static_cast<int64_t>(num_cus > 0 ? num_cus : 256) * hy::kPrefillWgPerCu;
-    double best = prefill_cost(tile_steps, max_steps, num_kv_heads, slots);
+    PrefillSim sim;
+    double best = sim.cost(tile_steps, rule, num_kv_heads, slots, HUGE_VAL);
     // Candidates: every length down to 2 steps for short ranges, at most 32
-    // evenly spaced ones for long ranges (the simulation is cheap).
-    const int64_t step = std::max<int64_t>(1, (max_steps - 2) / 32);
-    for (int64_t cand = max_steps - step; cand >= 2; cand -= step) {
-      const double t = prefill_cost(tile_steps, cand, num_kv_heads, slots);
-      if (t < best) {
-        best = t;
-        max_steps = cand;
+    // evenly spaced ones for long ranges (the simulation is cheap), each cut
+    // evenly and capped with a few remainder thresholds.
+    const int64_t top = rule.len;
+    const int64_t step = std::max<int64_t>(1, (top - 2) / 32);
+    for (int64_t len = top - step; len >= 2; len -= step) {
+      const SplitRule cands[] = {{false, len, 0}, {true, len, 1}, {true, len, 2},
+                                 {true, len, 4}, {true, len, 8}, {true, len, len / 2}};
+      for (const SplitRule &c : cands) {
+        const double t = sim.cost(tile_steps, c, num_kv_heads, slots, best);
+        if (t < best) {
+          best = t;
+          rule = c;
+        }
       }
     }
   }
@@ -288,15 +349,17 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
   };
   std::vector<PItem> pitems;
   int32_t n_pmerge = 0, n_pslots = 0;
+  std::vector<int64_t> lens;
   for (const Tile &t : tiles) {
-    const int64_t n = (t.steps + max_steps - 1) / max_steps;
-    const int64_t per = (t.steps + n - 1) / n;
-    int64_t parts = 0;
-    for (int64_t a = 0; a < t.steps; a += per) {
+    split_tile(t.steps, rule, lens);
+    const int64_t n = static_cast<int64_t>(lens.size());
+    int64_t parts = 0, a = 0;
+    for (int64_t len : lens) {
       const int32_t kv0 = static_cast<int32_t>(a * kPrefillKeys);
-      const int32_t kv1 = static_cast<int32_t>(std::min<int64_t>(t.kv_end, (a + per) * kPrefillKeys));
+      const int32_t kv1 = static_cast<int32_t>(std::min<int64_t>(t.kv_end, (a + len) * kPrefillKeys));
       pitems.push_back({t.seq, t.q0, t.q1, kv0, kv1, n > 1 ? n_pslots + static_cast<int32_t>(parts) : -1});
       ++parts;
+      a += len;
     }
     if (n > 1) {
       if (n_pmerge >= prefill_merge_capacity) {

@@ -127,28 +127,31 @@ def test_plan_chunk_cut_rounds_to_32_tokens():
     assert p.n_slots == 2 * W
 
 
-def test_plan_prefill_tiles_cover_every_query_and_key_once():
-    q = [512, 512, 1, 3, 512]
-    kv = [512, 4096, 700, 10, 8192]
-    p = plan(q, kv)
-    _, pieces = chunks_and_pieces(p)
+def check_prefill_cover(q, kv, p):
+    """Every query tile's key range [0, cache + q1) is covered once by its
+    parts, which start on 64-key steps and are dispatched longest first; a
+    split tile has one merge item over its parts' partial slots."""
     pre = p.prefill
-    assert len(pieces) >= 1 and (pieces[:, 0] == 2).all()
     tile = _native.lib().hy_prefill_tile_rows() // 4
     lengths = pre[:, 4] - pre[:, 3]
     assert (lengths[:-1] >= lengths[1:]).all()  # longest first
     assert (pre[:, 3] % 64 == 0).all()
     merges = {(int(m[0]), int(m[1])): m for m in p.prefill_merge}
-    for s_, ql in [(0, 512), (1, 512), (3, 3), (4, 512)]:
+    n_parts = 0
+    for s_, ql in enumerate(q):
+        if ql <= 1:
+            assert not (pre[:, 0] == s_).any()
+            continue
         cache = kv[s_] - ql
         rows = pre[pre[:, 0] == s_]
         for q0 in range(0, ql, tile):
             q1 = min(ql, q0 + tile)
             parts = rows[(rows[:, 1] == q0)]
+            n_parts += len(parts)
             assert (parts[:, 2] == q1).all()
             parts = parts[np.argsort(parts[:, 3])]
             assert parts[0, 3] == 0 and parts[-1, 4] == cache + q1
-            assert (parts[1:, 3] == parts[:-1, 4]).all()
+            assert (parts[1:, 3] == parts[:-1, 4]).all() and (parts[:, 4] > parts[:, 3]).all()
             if len(parts) == 1:
                 assert parts[0, 5] == -1 and (s_, q0) not in merges
             else:
@@ -156,9 +159,40 @@ def test_plan_prefill_tiles_cover_every_query_and_key_once():
                 assert m[2] == q1 and m[4] == len(parts)
                 assert m[5] == sum(q[:s_])  # q_start of the sequence
                 assert sorted(parts[:, 5]) == list(range(m[3], m[3] + len(parts)))
+    assert n_parts == len(pre)
     assert p.n_prefill_slots == int((pre[:, 5] >= 0).sum())
+    return merges
+
+
+def test_plan_prefill_tiles_cover_every_query_and_key_once():
+    q = [512, 512, 1, 3, 512]
+    kv = [512, 4096, 700, 10, 8192]
+    p = plan(q, kv)
+    _, pieces = chunks_and_pieces(p)
+    assert len(pieces) >= 1 and (pieces[:, 0] == 2).all()
     # the 8192-token tile must have been split to balance the tick
-    assert len(merges) > 0
+    assert len(check_prefill_cover(q, kv, p)) > 0
+
+
+@pytest.mark.parametrize("shape", ["prefill_4x512", "mixed_tick", "random0", "random1", "random2"])
+def test_plan_prefill_cover_across_shapes(shape):
+    """The split rules the planner picks from (even parts, or full parts of
+    a cap plus a shorter remainder) on the benchmark shapes and on random
+    chunked prefills."""
+    if shape == "prefill_4x512":
+        q, kv = [512] * 4, [512, 1536, 2560, 4096]
+    elif shape == "mixed_tick":
+        offs = [1280, 1920, 1280, 3072, 2944, 1152, 3968, 4096]
+        q, kv = [512] * 8 + [1] * 56, [o + 512 for o in offs] + [3000] * 56
+    else:
+        rng = np.random.default_rng(int(shape[-1]))
+        n = int(rng.integers(1, 12))
+        q = rng.integers(2, 1025, size=n).tolist()
+        kv = [x + int(rng.integers(0, 20000)) for x in q]
+    merges = check_prefill_cover(q, kv, plan(q, kv))
+    if shape == "prefill_4x512":
+        # the offset-3584 tiles (57-64 steps) cannot run whole on 32 CUs per kv head
+        assert any(k[0] == 3 for k in merges)
 
 
 def test_plan_rejects_bad_input():
