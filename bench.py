@@ -481,7 +481,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"decode_kernel<4, fused append> ({dk})",
+            "kernel": f"decode_kernel<4, {'true' if dk == 'hy_paged_decode_append' else 'false'}> ({dk})",
             "achieved": round(head["decode_GBps_kernel"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -497,7 +497,7 @@ def main():
     if pre and "prefill_TFLOPs_kernel" in pre:
         line["roofline_prefill"] = {
             "bound": "mfma",
-            "kernel": "prefill_kernel<4, 64> (hy_paged_prefill) on prefill_4x512",
+            "kernel": "prefill_kernel<4> (hy_paged_prefill) on prefill_4x512",
             "achieved": round(pre["prefill_TFLOPs_kernel"], 1),
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
