@@ -101,7 +101,7 @@ class KernelEvents:
                 for n in self.pool if self.used[n]}
 
 
-def time_workload(name, steps, warmup, layers, split=0, replays=5):
+def time_workload(name, steps, warmup, layers, split=0, replays=20):
     """Times `steps` steps eagerly (per-step events) and as `replays`
     replays of one captured K-step graph; returns a dict of medians."""
     from hayate_amd.workloads import make_workload
@@ -288,7 +288,7 @@ def time_engine(steps, warmup, which):
     graph.replay()
     torch.cuda.synchronize()
     replays = []
-    for _ in range(max(5, steps // 2)):
+    for _ in range(max(20, steps)):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         graph.replay()
