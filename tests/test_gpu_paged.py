@@ -526,6 +526,32 @@ def test_random_mixed_ticks(seed):
     assert_attention_close(bits(out), o_exp, f"random tick {seed}")
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_random_ticks_deep_prefixes_pages_and_groups(seed):
+    """Seeded random ticks over deeper prefixes (0-8,000 cached tokens, so
+    the planner cuts long prefill tiles into full parts plus a short
+    remainder), pages of 128 or 256 tokens (begin_tick keeps the reference's
+    128-token minimum; smaller pages go through the C ABI in
+    test_small_pages_through_the_c_abi) and GQA groups 1-16; pools and
+    rotated q bit-exact, attention within tolerance."""
+    rng = np.random.default_rng(2000 + seed)
+    hq, hkv = [(32, 8), (64, 8), (16, 8), (8, 8), (64, 4)][int(rng.integers(0, 5))]
+    page_size = [128, 256][int(rng.integers(0, 2))]
+    n = int(rng.integers(2, 7))
+    q_lens = [1 if rng.random() < 0.4 else int(rng.integers(2, 513)) for _ in range(n)]
+    cache_lens = [int(rng.integers(0, 8001)) for _ in range(n)]
+    say(f"[random deep tick seed={seed} hq={hq} hkv={hkv} page={page_size} q={q_lens} "
+        f"cache={cache_lens}]")
+    w = _custom_workload(hq, hkv, cache_lens, q_lens, page_size=page_size, seed=seed)
+    pre_k, pre_v = layer_bits(w.manager)
+    q_rot, out = gpu_step(w)
+    post_k, post_v = layer_bits(w.manager)
+    pk, pv, q_exp, o_exp = oracle_step(w, pre_k, pre_v)
+    assert np.array_equal(bits(q_rot), q_exp), "rotated q differs"
+    assert np.array_equal(post_k, pk) and np.array_equal(post_v, pv), "pools differ"
+    assert_attention_close(bits(out), o_exp, f"random deep tick {seed}")
+
+
 def test_few_key_rows_exact_base():
     """Rows that see 1-4 keys (the first tokens of a chunk at offset 0) put
     most weight on one key, so an error in that key's probability shows in
