@@ -116,8 +116,8 @@ struct PrefillSim {
       copies = 1;
     }
     // Lower bounds first: the longest part, and all the work spread evenly.
-    const double floor = std::max(longest, total * copies / static_cast<double>(slots)) + extra;
-    if (costs.empty() || floor >= bound) return floor;
+    const double lower = std::max(longest, total * copies / static_cast<double>(slots)) + extra;
+    if (costs.empty() || lower >= bound) return lower;
     std::sort(costs.begin(), costs.end(), std::greater<double>());
     free_at.assign(static_cast<size_t>(slots), 0.0);  // a min-heap (all equal)
     double makespan = 0.0;
