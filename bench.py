@@ -32,6 +32,7 @@ Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -101,12 +102,44 @@ class KernelEvents:
                 for n in self.pool if self.used[n]}
 
 
+def input_digests(w):
+    """The workload's seed and a SHA-256 of each generated input, taken
+    before any step runs: raw q/k/v, norm weights, rope tables, lengths and
+    page lists, and a fixed sample of the N(0, 1) pool (layer 0, kv head 0:
+    its first and last 4,096 token rows of K and V; the whole pool is
+    several GB)."""
+    def sha(t):
+        t = t.detach().contiguous()
+        if t.dtype == torch.bfloat16:
+            t = t.view(torch.int16)
+        return hashlib.sha256(t.cpu().numpy().tobytes()).hexdigest()
+
+    m = w.manager
+    n = min(4096, m.k_cache.shape[3])
+    lens = np.array([w.cache_lens, w.q_lens], dtype=np.int64)
+    pages = np.array([p for pl in w.page_lists for p in pl] + [-1] + [len(pl) for pl in w.page_lists],
+                     dtype=np.int64)
+    return {
+        "seed": w.spec.seed,
+        "sha256": {
+            "q": sha(w.q), "k": sha(w.k), "v": sha(w.v),
+            "q_norm_w": sha(w.q_norm_w), "k_norm_w": sha(w.k_norm_w),
+            "cos": sha(w.cos), "sin": sha(w.sin),
+            "cache_lens_q_lens": hashlib.sha256(lens.tobytes()).hexdigest(),
+            "page_lists": hashlib.sha256(pages.tobytes()).hexdigest(),
+            "pool_sample": sha(torch.cat([m.k_cache[0, 0, 0, :n], m.k_cache[0, 0, 0, -n:],
+                                          m.v_cache[0, 0, 0, :n], m.v_cache[0, 0, 0, -n:]])),
+        },
+    }
+
+
 def time_workload(name, steps, warmup, layers, split=0, replays=20):
     """Times `steps` steps eagerly (per-step events) and as `replays`
     replays of one captured K-step graph; returns a dict of medians."""
     from hayate_amd.workloads import make_workload
 
     w = make_workload(name, device="cuda", num_layers=layers, tokens_per_split=split)
+    inputs = input_digests(w)
     batch = w.begin()
     decode_only = all(ql == 1 for ql in w.q_lens)
     stream = torch.cuda.current_stream()
@@ -139,6 +172,7 @@ def time_workload(name, steps, warmup, layers, split=0, replays=20):
         "n_prefill_items": plan.n_prefill,
         "kernel_ms_median": kernel_ms,
         "decode_kernel": dec_kernel,
+        "inputs": inputs,
     }
     out.update(time_graphs(w, batch, steps, layers, decode_only, replays))
     step_ms = out["ms_per_step_graph"]
