@@ -51,6 +51,12 @@ constexpr double kPartialCost = 0.025;
 constexpr int kDecodeWgPerCu = 1;     // decode workgroups (chunks) per CU
 using hy::kDecodeWaves;                // waves per decode workgroup: partials per piece
 constexpr int64_t kMinChunk = 64;     // smallest decode chunk, in tokens (two slices)
+// Cost of a decode piece after a chunk's first, in tokens: per-wave stamps
+// (s_memrealtime) of the batch-32 decode on MI355X put a chunk at 43.4 /
+// 45.0 / 45.7 / 46.5 us with 1 / 2 / 3 / 4 pieces for the same tokens
+// (~1.1 us per piece: a partial flush, the next query rows and a partial
+// last slice) at ~0.0192 us per token.
+constexpr int64_t kDecodePieceCost = 64;
 
 // How a prefill tile of `steps` key steps is cut into key ranges (parts).
 // Even: the fewest parts of at most `len` steps, of equal length (+-1).
@@ -200,20 +206,26 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
   struct ChunkRec {
     int32_t piece_begin, piece_end, n_slices;
   };
-  std::vector<PieceRec> pieces;
-  std::vector<ChunkRec> chunks;
+  struct DecodeCut {
+    std::vector<PieceRec> pieces;
+    std::vector<ChunkRec> chunks;
+  };
   const int32_t max_pieces = hy::decode_max_pieces(G);
-  int32_t n_merge = 0, n_pre = 0;
-  {
-    int64_t pos = 0;          // stream position of the next token
+  // Cuts the decode stream into n_chunks chunks of equal cost, where a
+  // chunk's cost is its tokens plus `piece_cost` for every piece after its
+  // first, and `total` is the whole stream's cost.
+  auto cut_stream = [&](int64_t total, int64_t piece_cost, DecodeCut &d) {
+    d.pieces.clear();
+    d.chunks.clear();
+    int64_t pos = 0;          // stream cost before the next piece
     int64_t chunk = 0;        // index of the chunk being filled
-    int64_t chunk_start = 0;  // stream position where it began
+    int64_t chunk_start = 0;  // stream cost where it began
     int32_t first = 0;        // its first piece
     int32_t slices = 0;       // its slices so far
     auto close_chunk = [&]() {
-      if (static_cast<int32_t>(pieces.size()) > first)
-        chunks.push_back({first, static_cast<int32_t>(pieces.size()), slices});
-      first = static_cast<int32_t>(pieces.size());
+      if (static_cast<int32_t>(d.pieces.size()) > first)
+        d.chunks.push_back({first, static_cast<int32_t>(d.pieces.size()), slices});
+      first = static_cast<int32_t>(d.pieces.size());
       slices = 0;
       ++chunk;
       chunk_start = pos;
@@ -223,47 +235,83 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
     // early thus leaves its unfilled share to all later chunks instead of
     // moving every later cut one chunk ahead of the stream.
     auto chunk_target = [&]() -> int64_t {
-      return chunk_start + (decode_tokens - chunk_start) / (n_chunks - chunk);
+      return chunk_start + (total - chunk_start) / (n_chunks - chunk);
     };
     for (int b = 0; b < num_seqs; ++b) {
       if (q_lens[b] != 1) continue;
       const int64_t kv = kv_lens[b];
-      const int64_t seq_pos = pos;  // stream position of token 0
-      const int32_t seq_first = static_cast<int32_t>(pieces.size());
       int64_t t = 0;
       while (t < kv) {
+        // stream cost at token t once the piece's own cost is paid
+        const int64_t at =
+            pos + (static_cast<int32_t>(d.pieces.size()) > first ? piece_cost : 0);
         int64_t end = kv;
         bool cut = false;
         if (chunk < n_chunks - 1) {
           const int64_t chunk_end = chunk_target();
-          if (chunk_end - seq_pos < kv) {
-            end = std::min<int64_t>(kv, std::max<int64_t>(t, (chunk_end - seq_pos + kSlice / 2) /
-                                                               kSlice * kSlice));
+          if (chunk_end - at < kv - t) {
+            end = std::min<int64_t>(
+                kv, std::max<int64_t>(t, t + (chunk_end - at + kSlice / 2) / kSlice * kSlice));
             cut = true;
           }
         }
         if (end > t) {
-          pieces.push_back({b, static_cast<int32_t>(t), static_cast<int32_t>(end), slices});
+          d.pieces.push_back({b, static_cast<int32_t>(t), static_cast<int32_t>(end), slices});
           slices += static_cast<int32_t>((end - t + kSlice - 1) / kSlice);
-          pos += end - t;
+          pos = at + (end - t);
           t = end;
         }
         // A chunk also ends at the size of the kernel's query table.
-        if (cut || static_cast<int32_t>(pieces.size()) - first >= max_pieces) close_chunk();
+        if (cut || static_cast<int32_t>(d.pieces.size()) - first >= max_pieces) close_chunk();
       }
-      if (n_merge >= merge_capacity) {
-        hy::set_error("hy_plan_tick: merge capacity %d too small", merge_capacity);
-        return HY_ENOSPACE;
-      }
-      int32_t *mt = merge_items + 4 * n_merge++;
-      const int32_t np = static_cast<int32_t>(pieces.size()) - seq_first;
-      mt[0] = b;
-      mt[1] = kDecodeWaves * seq_first;
-      mt[2] = kDecodeWaves * np;
-      mt[3] = q_begin[b];
     }
-    if (static_cast<int32_t>(pieces.size()) > first)
-      chunks.push_back({first, static_cast<int32_t>(pieces.size()), slices});
+    if (static_cast<int32_t>(d.pieces.size()) > first)
+      d.chunks.push_back({first, static_cast<int32_t>(d.pieces.size()), slices});
+  };
+  // The costliest chunk: its slices' tokens plus kDecodePieceCost for every
+  // piece after its first.
+  auto max_chunk_cost = [&](const DecodeCut &d) {
+    int64_t worst = 0;
+    for (const ChunkRec &c : d.chunks)
+      worst = std::max<int64_t>(worst, static_cast<int64_t>(c.n_slices) * kSlice +
+                                           kDecodePieceCost * (c.piece_end - c.piece_begin - 1));
+    return worst;
+  };
+  // Equal tokens per chunk first; then cuts that price each extra piece,
+  // the stream's total cost taken from the previous cut's piece count; the
+  // cut with the cheapest costliest chunk is kept.
+  DecodeCut best, trial;
+  cut_stream(decode_tokens, 0, best);
+  int64_t best_cost = max_chunk_cost(best);
+  int64_t total = decode_tokens;
+  for (int pass = 0; pass < 3 && n_chunks > 1; ++pass) {
+    cut_stream(total, kDecodePieceCost, trial);
+    const int64_t c = max_chunk_cost(trial);
+    total = decode_tokens + kDecodePieceCost * static_cast<int64_t>(trial.pieces.size() -
+                                                                    trial.chunks.size());
+    if (c < best_cost) {
+      best_cost = c;
+      std::swap(best, trial);
+    }
+  }
+  const std::vector<PieceRec> &pieces = best.pieces;
+  const std::vector<ChunkRec> &chunks = best.chunks;
+  // One merge item per decode sequence over its pieces' slots (its pieces
+  // are consecutive).
+  int32_t n_merge = 0, n_pre = 0;
+  for (size_t i = 0; i < pieces.size();) {
+    size_t j = i;
+    while (j < pieces.size() && pieces[j].seq == pieces[i].seq) ++j;
+    if (n_merge >= merge_capacity) {
+      hy::set_error("hy_plan_tick: merge capacity %d too small", merge_capacity);
+      return HY_ENOSPACE;
+    }
+    int32_t *mt = merge_items + 4 * n_merge++;
+    mt[0] = pieces[i].seq;
+    mt[1] = kDecodeWaves * static_cast<int32_t>(i);
+    mt[2] = kDecodeWaves * static_cast<int32_t>(j - i);
+    mt[3] = q_begin[pieces[i].seq];
+    i = j;
   }
   const int32_t n_dec = static_cast<int32_t>(chunks.size());
   const int32_t n_pieces = static_cast<int32_t>(pieces.size());

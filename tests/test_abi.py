@@ -41,6 +41,7 @@ def plan(q, kv, hq=32, hkv=8, page=128, cus=256, split=0):
 
 
 W = 2  # waves per decode workgroup: partials per piece
+PIECE_COST = 64  # tokens the planner charges a decode piece after a chunk's first
 
 
 def chunks_and_pieces(p):
@@ -88,9 +89,29 @@ def test_plan_decode_covers_every_token_once(split):
         assert len(chunks) == -(-int(kv.sum()) // split)
     else:
         assert len(chunks) == 256 // 8
-    # equal chunks up to the rounding of each cut to 32 tokens (+-16 at
-    # either end)
-    assert max(tokens) - min(tokens) <= 65
+    # equal chunk costs (slices' tokens plus 64 per piece after a chunk's
+    # first) up to the rounding of each cut to 32 tokens at either end and a
+    # partial last slice
+    cost = chunks[:, 2] * 32 + PIECE_COST * (chunks[:, 1] - chunks[:, 0] - 1)
+    assert cost.max() - cost.min() <= 128
+
+
+def test_plan_decode_chunks_with_more_pieces_get_fewer_tokens():
+    """Batch-32 decode lengths (256-4,096): each piece after a chunk's first
+    costs a partial flush and a query switch, so the cut gives chunks with
+    more pieces fewer tokens, and no chunk costs more than an equal-token
+    cut's costliest chunk would."""
+    rng = np.random.default_rng(1002)
+    kv = rng.integers(256, 4097, size=32)
+    p = plan([1] * 32, kv)
+    chunks, pieces = chunks_and_pieces(p)
+    n = chunks[:, 1] - chunks[:, 0]
+    tokens = np.array([int((pieces[c[0]:c[1], 2] - pieces[c[0]:c[1], 1]).sum()) for c in chunks])
+    assert n.max() >= 3 and n.min() == 1
+    assert tokens[n == 1].mean() > tokens[n >= 3].mean() + 64
+    cost = chunks[:, 2] * 32 + PIECE_COST * (n - 1)
+    equal_share = -(-int(kv.sum()) // len(chunks))
+    assert cost.max() <= equal_share + 32 + PIECE_COST * (n.max() - 1)
 
 
 def test_plan_chunk_holds_at_most_the_query_table():
