@@ -2,10 +2,11 @@
 //
 // Work split: the K/V rows of all decode sequences, in sequence order, form
 // one token stream per kv head; the planner cuts it into chunks of equal
-// length, one per CU and kv head, so every workgroup streams the same number
-// of bytes whatever the spread of context lengths. A chunk holds one or more
-// pieces (the part of one sequence inside the chunk). Grid: (kv head,
-// chunk); with 8 kv heads, XCD i streams head i. A workgroup serves all
+// cost (tokens plus a fixed charge per extra piece), one per CU and kv head,
+// so every workgroup takes about the same time whatever the spread of
+// context lengths. A chunk holds one or more pieces (the part of one
+// sequence inside the chunk). Grid: (kv head, chunk); with 8 kv heads each
+// XCD streams one head. A workgroup serves all
 // G = num_q_heads / num_kv_heads query heads of its kv head from a single
 // read of every K/V row (GQA sharing).
 //

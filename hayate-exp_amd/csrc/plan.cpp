@@ -2,8 +2,9 @@
 // decode and prefill kernels consume. Host-only code, no device access.
 //
 // Decode sequences (q_len == 1): their K/V rows, concatenated in sequence
-// order, are cut into one chunk per CU and kv head, equal in length (cuts
-// inside a sequence on multiples of 32 tokens); each piece of a sequence in
+// order, are cut into one chunk per CU and kv head, equal in cost (tokens
+// plus a fixed charge for every piece after a chunk's first; cuts inside a
+// sequence on multiples of 32 tokens); each piece of a sequence in
 // a chunk gets W workspace slots (one per wave of the decode workgroup) and
 // every decode sequence one merge item over its pieces' slots.
 // Prefill sequences (q_len > 1) are cut into query tiles of kPrefillRows / G
@@ -183,7 +184,7 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
 
   // Decode: the K/V rows of all decode sequences, concatenated in sequence
   // order, form one token stream per kv head that is cut into n_chunks
-  // chunks of equal length, one workgroup each. A cut inside a sequence
+  // chunks of equal cost, one workgroup each. A cut inside a sequence
   // falls on a multiple of 32 tokens of that sequence. A chunk holds one or
   // more pieces (the part of one sequence inside the chunk); each wave of a
   // chunk's workgroup leaves one partial per piece, and the merge pass
