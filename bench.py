@@ -443,6 +443,14 @@ def traffic_from_profile(name):
     return _profile_value(name, "hbm_bytes_per_launch", int)
 
 
+def _rocprof_frac(name, work_per_launch, peak):
+    """Roofline fraction from the kernel-trace mean duration recorded in
+    profiles/<name>.md (`kernel_mean_ns = ...`): work per launch (bytes, or
+    flops / 1e3 for TFLOP/s) per ns over the peak (GB/s or TFLOP/s)."""
+    ns = _profile_value(name, "kernel_mean_ns", float)
+    return None if not ns else round(work_per_launch / ns / peak, 4)
+
+
 def _profile_value(name, key, cast):
     path = os.path.join(ROOT, "profiles", f"{name}.md")
     if not os.path.exists(path):
@@ -525,6 +533,10 @@ def main():
                       "dispatch latency; rocprofv3 kernel-only durations are in profiles/)",
             "algorithmic_bytes": head["decode_kernel_bytes"],
             "traffic": traffic_from_profile("decode_kernel_decode_b32"),
+            # the same fraction from the committed rocprofv3 kernel-trace mean
+            # (kernel time alone, no dispatch latency)
+            "frac_rocprof": _rocprof_frac("decode_kernel_decode_b32",
+                                          head["decode_kernel_bytes"], HBM_PEAK_GBS),
         },
     }
     pre = results.get("prefill_4x512")
@@ -541,6 +553,8 @@ def main():
             "source": "median of HIP events around each launch on its stream",
             "step_TFLOPs_graph": round(pre["prefill_TFLOPs_graph"], 1),
             "mfma_util": _profile_value("prefill_kernel_prefill_4x512", "mfma_util", float),
+            "frac_rocprof": _rocprof_frac("prefill_kernel_prefill_4x512",
+                                          pre["prefill_flops"] / 1e3, BF16_PEAK_TFLOPS),
         }
     if not args.no_engine:
         line["engine"] = {}

@@ -243,7 +243,7 @@ struct AppendArgs {
   const uint16_t *v;
   int64_t v_ss, v_st, v_sh;
   const uint16_t *q_w, *k_w;
-  float eps;
+  float q_eps, k_eps;
   const float *cos_t, *sin_t;
   int max_pos;  // rows of cos_t / sin_t
   const int32_t *cache_lens;
@@ -282,6 +282,10 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
   const int pb = ch[0];
   const int pe = ch[1];
   const int n_sl = ch[2];
+  // An empty chunk record (a fixed-size grid padded past the plan's chunks)
+  // owns no piece and no partial slot: the whole workgroup leaves before
+  // any barrier.
+  if (pe <= pb) return;
 
   // Wave index as a scalar: every per-slice address below is wave-uniform.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -425,7 +429,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
         unpack8(load16(q + seq * q_ss + static_cast<int64_t>(qt) * q_st + (h0 + hh) * q_sh +
                        l16 * 8),
                 x);
-        if (ap.q_w != nullptr) rms_norm8(x, ap.q_w, l16, ap.eps);
+        if (ap.q_w != nullptr) rms_norm8(x, ap.q_w, l16, ap.q_eps);
         if (cos_row != nullptr) rope8(x, cos_row, sin_row, l16);
         const u32x4 y = pack8_rne(x);
         *reinterpret_cast<u32x4 *>(sQ + (j * G + hh) * kHeadDim + l16 * 8) = y;
@@ -440,7 +444,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
           unpack8(load16(ap.k + seq * ap.k_ss + static_cast<int64_t>(qt) * ap.k_st +
                          kvh * ap.k_sh + l16 * 8),
                   x);
-          if (ap.k_w != nullptr) rms_norm8(x, ap.k_w, l16, ap.eps);
+          if (ap.k_w != nullptr) rms_norm8(x, ap.k_w, l16, ap.k_eps);
           if (cos_row != nullptr) rope8(x, cos_row, sin_row, l16);
           const u32x4 yk = pack8_rne(x);
           const u32x4 yv = load16(ap.v + seq * ap.v_ss + static_cast<int64_t>(qt) * ap.v_st +
@@ -684,8 +688,9 @@ int fill_append_args(const char *name, hy::AppendArgs &ap, void *q_out, int64_t 
                      int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
                      const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
                      int64_t v_stride_head, const void *q_norm_weight,
-                     const void *k_norm_weight, float eps, const float *cos_table,
-                     const float *sin_table, int32_t max_positions, const int32_t *cache_lens) {
+                     const void *k_norm_weight, float q_eps, float k_eps,
+                     const float *cos_table, const float *sin_table, int32_t max_positions,
+                     const int32_t *cache_lens) {
   HY_REQUIRE(q_out && k && v && cache_lens, "%s: null pointer argument", name);
   HY_REQUIRE((cos_table == nullptr) == (sin_table == nullptr),
              "cos_table and sin_table must both be given or both be NULL");
@@ -705,7 +710,8 @@ int fill_append_args(const char *name, hy::AppendArgs &ap, void *q_out, int64_t 
   ap.v_sh = v_stride_head;
   ap.q_w = static_cast<const uint16_t *>(q_norm_weight);
   ap.k_w = static_cast<const uint16_t *>(k_norm_weight);
-  ap.eps = eps;
+  ap.q_eps = q_eps;
+  ap.k_eps = k_eps;
   ap.cos_t = cos_table;
   ap.sin_t = sin_table;
   ap.max_pos = max_positions;
@@ -752,7 +758,8 @@ extern "C" int hy_paged_decode_append(
     void *q_out, int64_t qo_stride_seq, int64_t qo_stride_tok, int64_t qo_stride_head,
     const void *k, int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
     const void *v, int64_t v_stride_seq, int64_t v_stride_tok, int64_t v_stride_head,
-    const void *q_norm_weight, const void *k_norm_weight, float eps, const float *cos_table,
+    const void *q_norm_weight, const void *k_norm_weight, float q_eps, float k_eps,
+    const float *cos_table,
     const float *sin_table, int32_t max_positions, void *out, void *k_pool, void *v_pool,
     int64_t pool_head_stride, const int32_t *page_table, int64_t page_table_stride,
     const int32_t *q_start, const int32_t *cache_lens, const int32_t *decode_items,
@@ -764,7 +771,8 @@ extern "C" int hy_paged_decode_append(
   if (int rc = fill_append_args("hy_paged_decode_append", ap, q_out, qo_stride_seq,
                                 qo_stride_tok, qo_stride_head, k, k_stride_seq, k_stride_tok,
                                 k_stride_head, v, v_stride_seq, v_stride_tok, v_stride_head,
-                                q_norm_weight, k_norm_weight, eps, cos_table, sin_table,
+                                q_norm_weight, k_norm_weight, q_eps, k_eps, cos_table,
+                                sin_table,
                                 max_positions, cache_lens))
     return rc;
   return paged_decode_impl("hy_paged_decode_append", q, q_stride_seq, q_stride_tok,
@@ -838,7 +846,8 @@ extern "C" int hy_paged_decode_append_noalloc(
     void *q_out, int64_t qo_stride_seq, int64_t qo_stride_tok, int64_t qo_stride_head,
     const void *k, int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
     const void *v, int64_t v_stride_seq, int64_t v_stride_tok, int64_t v_stride_head,
-    const void *q_norm_weight, const void *k_norm_weight, float eps, const float *cos_table,
+    const void *q_norm_weight, const void *k_norm_weight, float q_eps, float k_eps,
+    const float *cos_table,
     const float *sin_table, int32_t max_positions, void *out, int64_t o_stride_seq,
     int64_t o_stride_tok, int64_t o_stride_head, void *k_pool, void *v_pool,
     int64_t pool_head_stride, const int32_t *page_table, int64_t page_table_stride,
@@ -848,6 +857,10 @@ extern "C" int hy_paged_decode_append_noalloc(
     int32_t page_size, float scale, void *stream) {
   hy::clear_error();
   HY_REQUIRE(n_slots >= 0 && num_q_heads >= 1, "item counts must be non-negative");
+  // The scratch keeps whatever the previous call left; a merge is only
+  // meaningful over partials this same call's decode launch wrote.
+  HY_REQUIRE(!(n_decode == 0 && n_merge > 0),
+             "merge items without decode items would merge stale scratch partials");
   const int64_t need = hy_decode_workspace_bytes(n_slots, num_q_heads, head_dim);
   if (need > HY_NOALLOC_SCRATCH_BYTES) {
     hy::set_error("hy_paged_decode_append_noalloc: %d partial slots x %d heads need %lld bytes, "
@@ -861,7 +874,8 @@ extern "C" int hy_paged_decode_append_noalloc(
   if (int rc = fill_append_args("hy_paged_decode_append_noalloc", ap, q_out, qo_stride_seq,
                                 qo_stride_tok, qo_stride_head, k, k_stride_seq, k_stride_tok,
                                 k_stride_head, v, v_stride_seq, v_stride_tok, v_stride_head,
-                                q_norm_weight, k_norm_weight, eps, cos_table, sin_table,
+                                q_norm_weight, k_norm_weight, q_eps, k_eps, cos_table,
+                                sin_table,
                                 max_positions, cache_lens))
     return rc;
   if (n_decode == 0 && n_merge == 0) return HY_OK;

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
     const uint16_t *__restrict__ k, int64_t k_ss, int64_t k_st, int64_t k_sh,
     const uint16_t *__restrict__ v, int64_t v_ss, int64_t v_st, int64_t v_sh,
     const uint16_t *__restrict__ q_w, const uint16_t *__restrict__ k_w,
-    float eps, const float *__restrict__ cos_t,
+    float q_eps, float k_eps, const float *__restrict__ cos_t,
     const float *__restrict__ sin_t, uint16_t *__restrict__ k_pool,
     uint16_t *__restrict__ v_pool, int64_t pool_hs,
     const int32_t *__restrict__ q_start, const int32_t *__restrict__ cache_lens,
@@ -162,6 +162,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
   // Every load is issued before the first use of any: rows, weights, the
   // token's sequence (scalar), the cos/sin row and the page (scalar).
   const uint16_t *w = is_q ? q_w : k_w;
+  const float eps = is_q ? q_eps : k_eps;
   u32x4 w_lo, w_hi;
   if (w != nullptr) {
     w_lo = load16(w + lane * 8);
@@ -345,7 +346,7 @@ extern "C" int hy_qknorm_rope_append(
     int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
     const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
     int64_t v_stride_head, const void *q_norm_weight,
-    const void *k_norm_weight, float eps, const float *cos_table,
+    const void *k_norm_weight, float q_eps, float k_eps, const float *cos_table,
     const float *sin_table, int32_t max_positions, void *k_pool, void *v_pool,
     int64_t pool_head_stride, const int32_t *q_start,
     const int32_t *cache_lens, const int32_t *page_table,
@@ -382,7 +383,7 @@ extern "C" int hy_qknorm_rope_append(
       k_stride_head, static_cast<const uint16_t *>(v), v_stride_seq,
       v_stride_tok, v_stride_head,
       static_cast<const uint16_t *>(q_norm_weight),
-      static_cast<const uint16_t *>(k_norm_weight), eps, cos_table, sin_table,
+      static_cast<const uint16_t *>(k_norm_weight), q_eps, k_eps, cos_table, sin_table,
       static_cast<uint16_t *>(k_pool), static_cast<uint16_t *>(v_pool),
       pool_head_stride, q_start, cache_lens, page_table, page_table_stride,
       num_seqs, total_tokens, num_q_heads, num_kv_heads, page_size, max_positions);

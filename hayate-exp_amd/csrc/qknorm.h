@@ -1,6 +1,6 @@
-// q/k RMSNorm and RoPE of one 128-element head row held by 16 lanes x 8
-// elements, shared by the append kernel and the decode kernel's fused
-// append. Every product and sum is rounded separately (the file that
+// q/k RMSNorm and RoPE of one 128-element head row, held by 16 lanes x 8
+// elements (the decode kernel's fused append) or by 8 lanes x 2 half rows
+// (the append kernel). Every product and sum is rounded separately (the file that
 // includes this must be built with -ffp-contract=off): the reference's
 // chain of elementwise torch ops rounds each step (hayate/model/rope.py:44-47),
 // so the results are bit-exact with it.
@@ -42,28 +42,10 @@ __device__ __forceinline__ uint32_t row_ror(uint32_t x) {
   static_assert(N >= 1 && N <= 15, "row_ror:1..15");
   return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x120 + N, 0xf, 0xf, false));
 }
-template <int N>
-__device__ __forceinline__ double row_ror_f64(double x) {
-  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(x));
-  const uint64_t lo = row_ror<N>(static_cast<uint32_t>(u));
-  const uint64_t hi = row_ror<N>(static_cast<uint32_t>(u >> 32));
-  return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
-}
 // Value of lane l ^ 8 of the row (a rotation by 8 of 16).
 __device__ __forceinline__ float row_xor8(float x) {
   return __uint_as_float(row_ror<8>(__float_as_uint(x)));
 }
-// Sum over the 16 lanes of a row, in every lane: rotations by 8, 4, 2, 1.
-// The terms are exact squares of bf16 values and fp64 holds their sum
-// exactly, so the order does not matter.
-__device__ __forceinline__ double row16_sum_f64(double x) {
-  x += row_ror_f64<8>(x);
-  x += row_ror_f64<4>(x);
-  x += row_ror_f64<2>(x);
-  x += row_ror_f64<1>(x);
-  return x;
-}
-
 // rsqrt(mean + eps) of a head row from its fp64 sum of squares: the mean
 // rounded to fp32, then sqrt and reciprocal each correctly rounded to fp32.
 __device__ __forceinline__ float rms_rstd(double ss, float eps) {
@@ -72,12 +54,32 @@ __device__ __forceinline__ float rms_rstd(double ss, float eps) {
   return static_cast<float>(1.0 / static_cast<double>(root));
 }
 
+// Sum over the 8 lanes of an aligned group, in every lane; defined with the
+// paired-half layout below.
+__device__ __forceinline__ double group8_sum_f64(double x);
+
 // wf: the 8 weights of this lane's features, already widened to fp32.
-__device__ __forceinline__ void rms_norm8(float (&x)[8], const float (&wf)[8], float eps) {
+// The sum of squares is accumulated in exactly the order rms_norm16 uses
+// for the same row: lane l < 8 and its partner l + 8 hold the two halves
+// rms_norm16's group lane l holds, so each interleaves its own and its
+// partner's squares (lo feature first) and both halves of the 16-lane row
+// reduce like one 8-lane group. The fp64 sum is exact for all but rows whose
+// squares span more than ~2^30; with one grouping the two layouts agree bit
+// for bit even then.
+__device__ __forceinline__ void rms_norm8(float (&x)[8], const float (&wf)[8], int lane,
+                                          float eps) {
+  const bool lo_half = lane < 8;
   double ss = 0.0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) ss += static_cast<double>(x[j] * x[j]);
-  const float rstd = rms_rstd(row16_sum_f64(ss), eps);
+  for (int j = 0; j < 8; ++j) {
+    const double own = static_cast<double>(x[j]);
+    const double other = static_cast<double>(row_xor8(x[j]));
+    const double a = lo_half ? own : other;
+    const double b = lo_half ? other : own;
+    ss = __builtin_fma(a, a, ss);
+    ss = __builtin_fma(b, b, ss);
+  }
+  const float rstd = rms_rstd(group8_sum_f64(ss), eps);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t w = pack_bf16x2_rne((x[2 * j] * rstd) * wf[2 * j],
@@ -92,7 +94,7 @@ __device__ __forceinline__ void rms_norm8(float (&x)[8],
                                           int lane, float eps) {
   float wf[8];
   unpack8(load16(w + lane * 8), wf);
-  rms_norm8(x, wf, eps);
+  rms_norm8(x, wf, lane, eps);
 }
 
 // y = bf16(x * cos + rotate_half(x) * sin), rotate_half(x) = cat(-x2, x1)

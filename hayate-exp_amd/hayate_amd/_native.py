@@ -43,7 +43,7 @@ _SIGNATURES = {
     ),
     "hy_qknorm_rope_append": (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P,
-         _I64, _I64, _I64, _P, _P, _F32, _P, _P, _I32, _P, _P, _I64, _P, _P,
+         _I64, _I64, _I64, _P, _P, _F32, _F32, _P, _P, _I32, _P, _P, _I64, _P, _P,
          _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P],
         ctypes.c_int,
     ),
@@ -69,7 +69,7 @@ _SIGNATURES = {
     ),
     "hy_paged_decode_append": (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64,
-         _I64, _P, _P, _F32, _P, _P, _I32, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _I32,
+         _I64, _P, _P, _F32, _F32, _P, _P, _I32, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _I32,
          _I32, _P, _I64, _I32, _I32, _I32, _I32, _I32, _F32, _P],
         ctypes.c_int,
     ),
@@ -79,7 +79,7 @@ _SIGNATURES = {
     ),
     "hy_paged_decode_append_noalloc": (
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64,
-         _I64, _P, _P, _F32, _P, _P, _I32, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P,
+         _I64, _P, _P, _F32, _F32, _P, _P, _I32, _P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P,
          _P, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _P],
         ctypes.c_int,
     ),
@@ -181,7 +181,9 @@ def plan_tick(
     dec_mask = q_lens == 1
     pre_mask = q_lens > 1
     dec_tokens = int(kv_lens[dec_mask].astype(np.int64).sum())
-    max_chunks = 2 * max(1, num_cus) + 1
+    # the planner takes num_cus <= 0 as 256 CUs
+    cus = num_cus if num_cus > 0 else 256
+    max_chunks = 2 * cus + 1
     if tokens_per_split > 0:
         max_chunks = max(max_chunks, dec_tokens // tokens_per_split + 1)
     # chunk records + piece records: a piece starts at every chunk boundary

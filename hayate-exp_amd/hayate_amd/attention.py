@@ -24,6 +24,27 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 
+# Number of fused q/k/v weight buffers built so far (any module).
+qkv_rebuilds = 0
+
+
+def _views_of(f: torch.Tensor, ws) -> bool:
+    """True when `ws` are consecutive row blocks of `f`, in order."""
+    row = 0
+    for w in ws:
+        n = w.shape[0]
+        if (w.device != f.device or w.dtype != f.dtype or w.shape[1:] != f.shape[1:]
+                or w.stride() != f.stride() or w.data_ptr() != f[row : row + n].data_ptr()):
+            return False
+        row += n
+    return row == f.shape[0]
+
+
+def _norm_eps(norm: nn.RMSNorm, dtype: torch.dtype) -> float:
+    """The epsilon nn.RMSNorm applies to inputs of `dtype`."""
+    return float(norm.eps) if norm.eps is not None else float(torch.finfo(dtype).eps)
+
+
 class GroupedQueryAttention(nn.Module):
     def __init__(self, d_in, num_heads, num_kv_groups, head_dim, dtype=None):
         super().__init__()
@@ -38,20 +59,35 @@ class GroupedQueryAttention(nn.Module):
         self.o_proj = nn.Linear(num_heads * head_dim, d_in, bias=False, dtype=dtype)
         self.q_norm = nn.RMSNorm(head_dim, eps=1e-6, dtype=dtype)
         self.k_norm = nn.RMSNorm(head_dim, eps=1e-6, dtype=dtype)
-        self._qkv_key = None
         self._qkv_weight = None
 
     def fused_qkv_weight(self) -> torch.Tensor:
-        """cat(q_proj.weight, k_proj.weight, v_proj.weight) along the output
-        dim, rebuilt whenever one of them is replaced or modified in place
-        (checkpoint loading copies into the parameters)."""
-        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
-        key = tuple((w.data_ptr(), w._version, w.device, w.dtype) for w in ws)
-        if key != self._qkv_key:
-            with torch.no_grad():
-                self._qkv_weight = torch.cat([w.detach() for w in ws], dim=0)
-            self._qkv_key = key
-        return self._qkv_weight
+        """The concatenated [W_q; W_k; W_v] (rows along the output dim), held
+        once: q_proj.weight, k_proj.weight and v_proj.weight are views of
+        it, so checkpoint loads and in-place updates of the parameters write
+        straight into the fused buffer and no second copy exists. The
+        buffer is (re)built, and the three parameters re-pointed into it,
+        the first time and whenever a parameter was replaced rather than
+        updated in place (module.to(), assignment); each rebuild advances
+        `qkv_rebuilds`, so holders of its address (captured graphs) can
+        tell."""
+        global qkv_rebuilds
+        lins = (self.q_proj, self.k_proj, self.v_proj)
+        f = self._qkv_weight
+        if f is not None and _views_of(f, [lin.weight for lin in lins]):
+            return f
+        # a normal tensor even when first called under inference_mode, so the
+        # parameters stay trainable and updatable in place
+        with torch.inference_mode(False), torch.no_grad():
+            f = torch.cat([lin.weight.detach() for lin in lins], dim=0)
+        row = 0
+        for lin in lins:
+            n = lin.weight.shape[0]
+            lin.weight = nn.Parameter(f[row : row + n], requires_grad=lin.weight.requires_grad)
+            row += n
+        self._qkv_weight = f
+        qkv_rebuilds += 1
+        return f
 
     def project_qkv(self, x):
         """x (B, T, d_in) -> q (B, T, Hq, D), k, v (B, T, Hkv, D): strided views
@@ -90,7 +126,10 @@ class GroupedQueryAttention(nn.Module):
         q, k, v = self.project_qkv(x)
         q_norm_w = self.q_norm.weight
         k_norm_w = self.k_norm.weight
-        eps = self.q_norm.eps if self.q_norm.eps is not None else torch.finfo(torch.float32).eps
+        # each norm keeps its own eps; None means the input dtype's epsilon,
+        # as nn.RMSNorm resolves it
+        eps = _norm_eps(self.q_norm, q.dtype)
+        k_eps = _norm_eps(self.k_norm, k.dtype)
         if paged_cache.varlen:
             # Varlen ticks carry packed tokens: x is (1, N, d_in).
             if B != 1:
@@ -98,22 +137,24 @@ class GroupedQueryAttention(nn.Module):
             if all(ql == 1 for ql in paged_cache.q_lens):
                 # a decode tick: norm, rope, append and attention in one launch
                 _, context = paged_cache.decode_layer(
-                    layer_idx, q[0], k[0], v[0], q_norm_w, k_norm_w, eps, cos, sin
+                    layer_idx, q[0], k[0], v[0], q_norm_w, k_norm_w, eps, cos, sin,
+                    k_eps=k_eps,
                 )
             else:
                 q_rot = paged_cache.norm_rope_write_layer(
-                    layer_idx, q[0], k[0], v[0], q_norm_w, k_norm_w, eps, cos, sin
+                    layer_idx, q[0], k[0], v[0], q_norm_w, k_norm_w, eps, cos, sin,
+                    k_eps=k_eps,
                 )
                 context = paged_cache.attend_layer(q_rot, layer_idx)
             context = context.unsqueeze(0)
         elif T == 1:
             _, context = paged_cache.decode_layer(
-                layer_idx, q, k, v, q_norm_w, k_norm_w, eps, cos, sin
+                layer_idx, q, k, v, q_norm_w, k_norm_w, eps, cos, sin, k_eps=k_eps
             )
             context = context.transpose(1, 2)
         else:
             q_rot = paged_cache.norm_rope_write_layer(
-                layer_idx, q, k, v, q_norm_w, k_norm_w, eps, cos, sin
+                layer_idx, q, k, v, q_norm_w, k_norm_w, eps, cos, sin, k_eps=k_eps
             )
             context = paged_cache.attend_layer(q_rot.transpose(1, 2), layer_idx).transpose(1, 2)
         context = context.reshape(B, T, self.num_heads * self.head_dim)

@@ -11,13 +11,17 @@ keeps all of it in device buffers that never move and rewrites them in
 place (one host-to-device copy per tick); the graph captured over one tick
 then computes the next.
 
-The planner's decode grid (chunks per kv head) is part of the captured
-launch, so a graph is kept per (batch size, chunk count); the chunk count
-only changes while the batch's total context is under one chunk per CU
-(64 tokens each), and a new count is captured once. The partial-result
-workspace and the work-list buffers are sized for the largest plan of the
-batch size, and the kernels are told that size (their workspace layout
-depends on it), so every tick's plan fits the captured layout.
+The decode grid is part of the captured launch, so it is fixed at the
+largest chunk count a plan can have (one chunk per CU and kv head); a
+tick whose plan has fewer chunks pads the list with empty chunk records,
+whose workgroups leave at once. One graph per batch size therefore serves
+every tick. The partial-result workspace and the work-list buffers are
+sized for the largest plan of the batch size, and the kernels are told
+that size (their workspace layout depends on it), so every tick's plan
+fits the captured layout. A graph reads the fused q/k/v weights by
+address; if a layer rebuilds them (its projection parameters were
+replaced, not updated in place), the graphs are dropped and captured
+again.
 
 This is what the reference's ``Engine(compile=True)`` (engine.py:84-90,
 torch.compile with CUDA graphs in "reduce-overhead" mode) buys on its path:
@@ -33,7 +37,7 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-from . import _native
+from . import _native, attention
 from .paged_cache import PagedCacheHandle, PagedKVBatch, PagedKVCacheManager, _require_hip
 
 
@@ -155,8 +159,9 @@ class StaticDecodeBatch(PagedKVBatch):
         host = _native.plan_tick(np.ones(B, dtype=np.int32), np.asarray(kv, dtype=np.int32),
                                  self.num_q_heads, self.num_kv_heads, self.page_size,
                                  self._num_cus, self.tokens_per_split)
-        if (len(host.decode) > self.record_capacity or host.n_slots > self.slot_capacity
-                or len(host.merge) != B):
+        n_pieces = len(host.decode) - host.n_chunks
+        if (host.n_chunks > self.max_chunks or self.max_chunks + n_pieces > self.record_capacity
+                or host.n_slots > self.slot_capacity or len(host.merge) != B):
             return False
         if self._copied is not None:
             self._copied.synchronize()  # the staging buffer is free again
@@ -168,15 +173,21 @@ class StaticDecodeBatch(PagedKVBatch):
         buf[self._off_cache : self._off_cache + B] = cache
         buf[self._off_kv : self._off_kv + B] = kv
         buf[self._off_qs : self._off_qs + B + 1] = np.arange(B + 1, dtype=np.int32)
-        dec = host.decode.reshape(-1)
-        buf[self._off_dec : self._off_dec + dec.size] = dec
+        # chunk records, empty ones up to the fixed grid, then the pieces
+        # (the kernel finds them after max_chunks records)
+        nc = host.n_chunks
+        dec = buf[self._off_dec : self._off_merge].reshape(-1, 8)
+        dec[:nc] = host.decode[:nc]
+        dec[nc : self.max_chunks] = 0
+        dec[nc : self.max_chunks, 0:2] = n_pieces  # piece_begin == piece_end: empty
+        dec[self.max_chunks : self.max_chunks + n_pieces] = host.decode[nc:]
         buf[self._off_merge : self._off_merge + 4 * B] = host.merge.reshape(-1)
         self._dev.copy_(self._host, non_blocking=True)
         self._copied = torch.cuda.Event()
         self._copied.record()
         self.cache_lens.copy_(self.cache_lens_i32, non_blocking=True)
         self._table_np = table
-        self._plan.n_decode = host.n_chunks
+        self._plan.n_decode = self.max_chunks
         self.cache_lens_host = cache
         self.kv_lens_host = kv
         self._max_kv = max(kv)
@@ -206,10 +217,15 @@ class DecodeGraphRunner:
                 "batch": StaticDecodeBatch(self.manager, batch_size, self.model.num_heads,
                                            self.max_tokens),
                 "ids": torch.zeros((1, batch_size), dtype=torch.long, device=self.manager.device),
-                "graphs": {},
+                "graph": None,
             }
             self._states[batch_size] = st
         return st
+
+    def drop_graphs(self) -> None:
+        """Forgets every captured graph (their memory pools go with them)."""
+        for st in self._states.values():
+            st["graph"] = None
 
     def _forward(self, st):
         with torch.inference_mode():
@@ -226,8 +242,10 @@ class DecodeGraphRunner:
             return None  # let the eager path raise its error
         st["ids"].copy_(torch.tensor(token_ids, dtype=torch.long).view(1, -1),
                         non_blocking=True)
-        key = batch.plan(self.model.num_heads).n_decode
-        entry = st["graphs"].get(key)
+        entry = st["graph"]
+        if entry is not None and entry[2] != attention.qkv_rebuilds:
+            self.drop_graphs()  # a fused q/k/v weight moved: recapture
+            entry = None
         if entry is None:
             stream = torch.cuda.current_stream()
             side = torch.cuda.Stream()
@@ -238,10 +256,12 @@ class DecodeGraphRunner:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 logits = self._forward(st)
-            entry = (graph, logits)
-            st["graphs"][key] = entry
+            # the warm-up and the capture may build fused weights: key on
+            # the count after them
+            entry = (graph, logits, attention.qkv_rebuilds)
+            st["graph"] = entry
             self.captures += 1
-        graph, logits = entry
+        graph, logits, _ = entry
         graph.replay()
         self.replays += 1
         return logits

@@ -158,7 +158,9 @@ class Engine:
         if stop_token_ids is None:
             stop_token_ids = _stop_token_ids(model_dir, tokenizer)
         self.scheduler = Scheduler(max_batch_size)
-        self.prefix_cache = PrefixCache(prefix_cache_max_tokens) if enable_prefix_cache else None
+        # one trie level of the prefix index per KV page
+        self.prefix_cache = (PrefixCache(prefix_cache_max_tokens, block_tokens=kv_page_size)
+                             if enable_prefix_cache else None)
         self.sampler = Sampler(tokenizer, stop_token_ids,
                                torch.Generator(device=self.device).manual_seed(seed))
         self.paged_cache = PagedKVCacheManager(

@@ -361,17 +361,19 @@ class PagedKVBatch:
         eps: float,
         cos: Optional[torch.Tensor],
         sin: Optional[torch.Tensor],
+        k_eps: Optional[float] = None,
     ) -> torch.Tensor:
         """Fused q/k RMSNorm + RoPE + paged append of k and v
         (attention.py:62-75 with rope.py:31-47). Inputs are the projection
         outputs, (B, T, H, D) (or packed (N, H, D) for a varlen tick); positions
-        are cache_lens + token index. Returns the rotated q in the same
-        layout; k and v go to the pool only."""
+        are cache_lens + token index. `eps` is the q norm's epsilon and
+        `k_eps` the k norm's (default: `eps`). Returns the rotated q in the
+        same layout; k and v go to the pool only."""
         a = self._append_inputs("norm_rope_write_layer", q, k, v, q_norm_weight,
                                 k_norm_weight, cos, sin)
         k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
         rc = _native.lib().hy_qknorm_rope_append(
-            *a.head, float(eps), *a.tables,
+            *a.head, float(eps), float(eps if k_eps is None else k_eps), *a.tables,
             k_ptr, v_ptr, hs,
             self._q_start_ptr, self._cache_lens_ptr, self._pt_ptr, self._pt_stride,
             self.num_seqs, self.total_tokens, a.num_q_heads, self.num_kv_heads,
@@ -439,6 +441,7 @@ class PagedKVBatch:
         sin: Optional[torch.Tensor],
         scale: Optional[float] = None,
         no_alloc: bool = False,
+        k_eps: Optional[float] = None,
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """norm_rope_write_layer then attend_layer, for a batch whose
         sequences all decode one token, in one kernel launch plus the merge
@@ -446,6 +449,7 @@ class PagedKVBatch:
         norm_rope_write_layer; returns (q_rot, out) exactly as the two calls
         would: q_rot in the input layout, out as attend_layer returns it.
         Pool contents and q_rot are bit-identical to the two-call path.
+        `eps` / `k_eps` are the q and k norms' epsilons, as there.
 
         no_alloc=True runs both launches through
         hy_paged_decode_append_noalloc, whose partials live in the library's
@@ -475,9 +479,10 @@ class PagedKVBatch:
         k_ptr, v_ptr, hs = self._layer_pools(layer_idx)
         stream = _stream_handle(self.device)
         lib = _native.lib()
+        eps_pair = (float(eps), float(eps if k_eps is None else k_eps))
         if no_alloc:
             self._launch("hy_paged_decode_append_noalloc", lib.hy_paged_decode_append_noalloc,
-                *a.head, float(eps), *a.tables, result.data_ptr(), *os_, k_ptr, v_ptr, hs,
+                *a.head, *eps_pair, *a.tables, result.data_ptr(), *os_, k_ptr, v_ptr, hs,
                 self._pt_ptr, self._pt_stride, self._q_start_ptr, self._cache_lens_ptr,
                 plan.decode_ptr, plan.n_decode, plan.merge_ptr, plan.n_merge, plan.n_slots,
                 self.num_seqs, num_q_heads, self.num_kv_heads, self.head_dim, self.page_size,
@@ -485,7 +490,7 @@ class PagedKVBatch:
             )
             return a.q_out, result
         self._launch("hy_paged_decode_append", lib.hy_paged_decode_append,
-            *a.head, float(eps), *a.tables, result.data_ptr(), k_ptr, v_ptr, hs,
+            *a.head, *eps_pair, *a.tables, result.data_ptr(), k_ptr, v_ptr, hs,
             self._pt_ptr, self._pt_stride, self._q_start_ptr, self._cache_lens_ptr,
             plan.decode_ptr, plan.n_decode, plan.n_slots, plan.workspace_ptr,
             plan.workspace_bytes, self.num_seqs, num_q_heads, self.num_kv_heads,

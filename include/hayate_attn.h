@@ -67,6 +67,8 @@ int hy_kv_append(void *k_pool, void *v_pool, int64_t pool_head_stride,
  * Fused per-head RMSNorm + rotary embedding of q and k, then paged append of
  * k and v. For token i of sequence b at position pos = cache_lens[b] + i:
  *   x' = bf16((x * (1 / sqrt(mean(x^2) + eps))) * w)          (fp32 math)
+ * with eps = q_eps for q rows and k_eps for k rows (the two RMSNorm modules
+ * of attention.py:34-35 each carry their own eps).
  *   y  = bf16(x' * cos[pos] + rotate_half(x') * sin[pos])       (fp32 math)
  * q' goes to q_out; k' and v (unchanged) are appended as hy_kv_append does.
  * q_norm_weight / k_norm_weight may be NULL (no norm); cos_table/sin_table
@@ -85,7 +87,8 @@ int hy_qknorm_rope_append(
     int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
     const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
     int64_t v_stride_head, const void *q_norm_weight,
-    const void *k_norm_weight, float eps, const float *cos_table,
+    const void *k_norm_weight, float q_eps, float k_eps,
+    const float *cos_table,
     const float *sin_table, int32_t max_positions, void *k_pool, void *v_pool,
     int64_t pool_head_stride, const int32_t *q_start,
     const int32_t *cache_lens, const int32_t *page_table,
@@ -182,7 +185,11 @@ int64_t hy_decode_workspace_bytes(int32_t n_slots, int32_t num_q_heads,
  * and read by the merge).
  * Causal semantics: the query of sequence b at position kv_len - 1 sees
  * every key k < kv_len (paged_cache.py:266-271). n_decode is at most 65535
- * (the grid's y limit); more returns HY_EINVAL.
+ * (the grid's y limit); more returns HY_EINVAL. The chunk records may be
+ * followed by empty ones (piece_begin == piece_end) up to n_decode, which
+ * do nothing: a caller that captures the launch in a graph can pass a fixed
+ * n_decode and pad the plan's records (the piece records then start after
+ * all n_decode chunk records).
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T == 1.
  */
 int hy_paged_decode(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
@@ -220,7 +227,8 @@ int hy_paged_decode_append(
     int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
     const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
     int64_t v_stride_head, const void *q_norm_weight,
-    const void *k_norm_weight, float eps, const float *cos_table,
+    const void *k_norm_weight, float q_eps, float k_eps,
+    const float *cos_table,
     const float *sin_table, int32_t max_positions, void *out, void *k_pool,
     void *v_pool, int64_t pool_head_stride, const int32_t *page_table,
     int64_t page_table_stride, const int32_t *q_start,
@@ -267,7 +275,8 @@ int hy_paged_decode_append_noalloc(
     int64_t k_stride_seq, int64_t k_stride_tok, int64_t k_stride_head,
     const void *v, int64_t v_stride_seq, int64_t v_stride_tok,
     int64_t v_stride_head, const void *q_norm_weight,
-    const void *k_norm_weight, float eps, const float *cos_table,
+    const void *k_norm_weight, float q_eps, float k_eps,
+    const float *cos_table,
     const float *sin_table, int32_t max_positions, void *out,
     int64_t o_stride_seq, int64_t o_stride_tok, int64_t o_stride_head,
     void *k_pool, void *v_pool, int64_t pool_head_stride,

@@ -155,14 +155,15 @@ def apply_rope(x_bits: np.ndarray, cos: np.ndarray, sin: np.ndarray, positions) 
 
 
 def qknorm_rope_append(q, k, v, q_w, k_w, eps, cos, sin, pool_k, pool_v, page_lists,
-                       cache_lens, q_lens, page_size):
+                       cache_lens, q_lens, page_size, k_eps=None):
     """attention.py:62-75 on packed tokens: q/k RMSNorm, RoPE at positions
-    cache_len + i, append of k and v. Returns the rotated q (bf16 bits)."""
+    cache_len + i, append of k and v. Returns the rotated q (bf16 bits).
+    `eps` is q_norm's epsilon, `k_eps` k_norm's (default: the same)."""
     positions = np.concatenate(
         [np.arange(c, c + n, dtype=np.int64) for c, n in zip(cache_lens, q_lens)]
     )
     qn = rms_norm(q, q_w, eps) if q_w is not None else q
-    kn = rms_norm(k, k_w, eps) if k_w is not None else k
+    kn = rms_norm(k, k_w, eps if k_eps is None else k_eps) if k_w is not None else k
     if cos is not None:
         qn = apply_rope(qn, cos, sin, positions)
         kn = apply_rope(kn, cos, sin, positions)

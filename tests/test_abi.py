@@ -284,3 +284,31 @@ def test_plan_short_decode_spreads_over_64_token_chunks():
     p = plan([1] * 4, [4096] * 4)
     assert len(plan([1] * 4, [4096] * 4).decode) - p.n_chunks >= 4
     assert p.n_chunks == 256 // 8  # capped at one chunk per CU and kv head
+
+
+def test_noalloc_rejects_merge_items_without_decode_items():
+    """With no decode items the static scratch holds the previous call's
+    partials; merging them would be silent garbage, so it is an argument
+    error, returned before any device work."""
+    lib = _native.lib()
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    args = [fake, 0, 0, 0, fake, 0, 0, 0, fake, 0, 0, 0, fake, 0, 0, 0, fake, fake, 1e-6, 1e-6,
+            fake, fake, 40960, fake, 0, 0, 0, fake, fake, 0, fake, 0, fake, fake,
+            fake, 0, fake, 3, 4, 1, 32, 8, 128, 128, 0.1, None]
+    rc = lib.hy_paged_decode_append_noalloc(*args)
+    assert rc == _native.HY_EINVAL
+    assert "stale" in _native.last_error()
+    with pytest.raises(ValueError):
+        _native.check(rc, "hy_paged_decode_append_noalloc")
+
+
+def test_plan_with_default_cu_count_sizes_its_buffers():
+    """num_cus <= 0 means 256 CUs to the planner; the record buffers are
+    sized the same way, so a deep decode batch plans without ENOSPACE."""
+    rng = np.random.default_rng(5)
+    for n in (1, 7, 32, 64):
+        kv = rng.integers(1, 12000, size=n)
+        p = plan([1] * n, kv, cus=0)
+        ref = plan([1] * n, kv, cus=256)
+        assert p.n_chunks == ref.n_chunks
+        assert np.array_equal(p.decode, ref.decode) and np.array_equal(p.merge, ref.merge)

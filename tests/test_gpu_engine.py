@@ -238,7 +238,9 @@ def test_compiled_engine_replays_decode_graphs_like_eager():
     assert eager.decode_graphs is None
     runner = graphs.decode_graphs
     say(f"  captures {runner.captures}, replays {runner.replays}")
-    assert runner.captures >= 3 and runner.replays >= 25
+    # one capture per batch size, although the plan's chunk count changes
+    # every 64 tokens of total context at these lengths
+    assert runner.captures == 3 and runner.replays >= 25
     assert t_graph == t_eager
     assert graphs.paged_cache.free_page_count == graphs.paged_cache.num_pages
 

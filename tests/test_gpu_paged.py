@@ -388,6 +388,50 @@ def test_fused_decode_append_ragged_and_many_short_sequences():
         assert_attention_close(bits(out_f), o_exp, "fused ragged")
 
 
+def test_fused_decode_append_wide_dynamic_range_rows():
+    """q and k rows whose magnitudes spread log-uniformly over 1e-6 .. 1e2
+    (squares over 2^53 apart, so the fp64 sums of squares round): the two
+    append layouts still accumulate in one order, so the fused decode and
+    the two-call path agree bit for bit; different q and k epsilons reach
+    their own norms."""
+    say("[fused decode, wide-range rows, q eps != k eps]")
+    g = torch.Generator().manual_seed(77)
+
+    def wide(shape):
+        mag = torch.pow(10.0, torch.empty(shape).uniform_(-6, 2, generator=g))
+        sign = torch.where(torch.rand(shape, generator=g) < 0.5, -1.0, 1.0)
+        return (mag * sign).to(torch.bfloat16).to(DEV)
+
+    w_a = make_workload("decode_b32", device=DEV)
+    w_b = make_workload("decode_b32", device=DEV)
+    q, k = wide(tuple(w_a.q.shape)), wide(tuple(w_a.k.shape))
+    for w in (w_a, w_b):
+        w.q, w.k = q, k
+    pre_k, pre_v = layer_bits(w_a.manager)
+    ba = w_a.begin()
+    q_f, out_f = ba.decode_layer(0, w_a.q, w_a.k, w_a.v, w_a.q_norm_w, w_a.k_norm_w, 1e-6,
+                                 w_a.cos, w_a.sin, k_eps=1e-3)
+    bb = w_b.begin()
+    q_s = bb.norm_rope_write_layer(0, w_b.q, w_b.k, w_b.v, w_b.q_norm_w, w_b.k_norm_w, 1e-6,
+                                   w_b.cos, w_b.sin, k_eps=1e-3)
+    out_s = bb.attend_layer(q_s, 0)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(q_f), bits(q_s)), "rotated q differs"
+    ka, va = layer_bits(w_a.manager)
+    kb, vb = layer_bits(w_b.manager)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb), "pools differ"
+    assert np.array_equal(bits(out_f), bits(out_s)), "attention differs"
+    # the k rows were normed with k_eps: the oracle with eps 1e-3 on k only
+    pk, pv = pre_k.copy(), pre_v.copy()
+    cos, sin = w_a.cos.cpu().numpy(), w_a.sin.cpu().numpy()
+    R.qknorm_rope_append(bits(q), bits(k), bits(w_a.v), bits(w_a.q_norm_w), bits(w_a.k_norm_w),
+                         1e-6, cos, sin, pk, pv, w_a.page_lists, w_a.cache_lens, w_a.q_lens,
+                         w_a.manager.page_size, k_eps=1e-3)
+    diff = np.count_nonzero(ka != pk)
+    say(f"  K rows vs oracle with k_eps: {diff} differing bf16 values")
+    assert diff == 0
+
+
 def test_fused_decode_graph_replay_matches_eager():
     say("[graph replay decode_layer]")
     w = make_workload("decode_b32", device=DEV, num_layers=1)

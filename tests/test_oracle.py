@@ -298,7 +298,8 @@ def test_attention_mutations_are_caught():
 
 # ------------------------------------------------- fused norm + rope + append
 def _reference_chain(q, k, v, q_w, k_w, cos, sin, pool_k, pool_v, page_lists, cache_lens,
-                     page_size, rope_first=False, positions_from_zero=False):
+                     page_size, rope_first=False, positions_from_zero=False, q_eps=1e-6,
+                     k_eps=1e-6):
     """The reference's op chain for one paged layer on a uniform (B, T)
     batch, written with the torch ops it uses:
     nn.RMSNorm on (B, T, H, D) (attention.py:34-35, 62-63), transpose to
@@ -308,8 +309,8 @@ def _reference_chain(q, k, v, q_w, k_w, cos, sin, pool_k, pool_v, page_lists, ca
     Mutations (for the sensitivity checks): rope_first rotates before the
     norm; positions_from_zero drops cache_lens from the positions."""
     B, T, _, D = q.shape
-    qn = torch.nn.RMSNorm(D, eps=1e-6, dtype=torch.bfloat16)
-    kn = torch.nn.RMSNorm(D, eps=1e-6, dtype=torch.bfloat16)
+    qn = torch.nn.RMSNorm(D, eps=q_eps, dtype=torch.bfloat16)
+    kn = torch.nn.RMSNorm(D, eps=k_eps, dtype=torch.bfloat16)
     with torch.no_grad():
         qn.weight.copy_(q_w)
         kn.weight.copy_(k_w)
@@ -389,3 +390,37 @@ def test_qknorm_rope_append_matches_reference_op_chain():
         assert not np.array_equal(
             q_ours, R.torch_bf16_to_bits(q_mut.transpose(1, 2).reshape(B * T, Hq, D))), mutation
         assert not np.array_equal(ok_k, R.torch_bf16_to_bits(mk)), mutation
+
+
+def test_qknorm_rope_append_separate_q_and_k_eps():
+    """The q and k norms are separate nn.RMSNorm modules, each with its own
+    eps (attention.py:34-35): with k_eps != eps the oracle matches the
+    reference chain built with those two modules, and differs from the
+    chain that uses q's eps for k."""
+    B, T, Hq, Hkv, D, P = 2, 3, 4, 2, 128, 8
+    cache_lens = [5, 0]
+    page_lists = [[3], [1]]
+    g = torch.Generator().manual_seed(43)
+    q = (torch.randn(B, T, Hq, D, generator=g) * 0.05).to(torch.bfloat16)
+    k = (torch.randn(B, T, Hkv, D, generator=g) * 0.05).to(torch.bfloat16)
+    v = torch.randn(B, T, Hkv, D, generator=g).to(torch.bfloat16)
+    q_w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    k_w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    cos_np, sin_np = R.rope_tables(D, 1_000_000, 64)
+    cos, sin = torch.from_numpy(cos_np), torch.from_numpy(sin_np)
+    pool0 = torch.randn(Hkv, 4 * P, D, generator=g).to(torch.bfloat16)
+    tk, tv = pool0.clone(), pool0.clone()
+    q_ref = _reference_chain(q, k, v, q_w, k_w, cos, sin, tk, tv, page_lists, cache_lens, P,
+                             q_eps=1e-6, k_eps=1e-2)
+    ok_k, ok_v = R.torch_bf16_to_bits(pool0).copy(), R.torch_bf16_to_bits(pool0).copy()
+    q_ours = R.qknorm_rope_append(
+        R.torch_bf16_to_bits(q.reshape(B * T, Hq, D)), R.torch_bf16_to_bits(k.reshape(B * T, Hkv, D)),
+        R.torch_bf16_to_bits(v.reshape(B * T, Hkv, D)), R.torch_bf16_to_bits(q_w),
+        R.torch_bf16_to_bits(k_w), 1e-6, cos_np, sin_np, ok_k, ok_v, page_lists, cache_lens,
+        [T] * B, P, k_eps=1e-2)
+    assert np.array_equal(q_ours, R.torch_bf16_to_bits(q_ref.transpose(1, 2).reshape(B * T, Hq, D)))
+    assert np.array_equal(ok_k, R.torch_bf16_to_bits(tk))
+    mk, mv = pool0.clone(), pool0.clone()
+    _reference_chain(q, k, v, q_w, k_w, cos, sin, mk, mv, page_lists, cache_lens, P,
+                     q_eps=1e-6, k_eps=1e-6)
+    assert not np.array_equal(ok_k, R.torch_bf16_to_bits(mk))

@@ -77,3 +77,110 @@ def test_paged_entries_hold_and_release_page_references():
     assert c.evict_lru() and not c.evict_lru()
     m.release(g)
     assert m.free_page_count == m.num_pages
+
+
+class _Stored:
+    """A stand-in entry: remembers which put() it came from and its length;
+    reset() records that the cache let go of it."""
+
+    released = []
+
+    def __init__(self, tag, length):
+        self.tag, self.length = tag, length
+
+    def slice(self, n, clone=False):
+        return _Stored(self.tag, n)
+
+    def reset(self):
+        _Stored.released.append(self.tag)
+
+
+class _LinearScan:
+    """The reference's lookup, restated as the plain scan it is
+    (prefix_cache.py:32-100): compare the prompt with every stored key in
+    least-recently-used order, keep the first strictly longer common prefix
+    (at most the limit), move the hit to the most recent end; put replaces
+    an identical key and evicts from the least recent end past the budget."""
+
+    def __init__(self, budget):
+        self.budget, self.keys, self.tags = budget, [], []
+
+    def get(self, tokens, limit):
+        limit = len(tokens) if limit is None else min(len(tokens), limit)
+        best, at = 0, None
+        for i, key in enumerate(self.keys):
+            n = 0
+            while n < min(len(key), limit) and key[n] == tokens[n]:
+                n += 1
+            if n > best:
+                best, at = n, i
+        if at is None:
+            return 0, None
+        self.keys.append(self.keys.pop(at))
+        self.tags.append(self.tags.pop(at))
+        return best, self.tags[-1]
+
+    def put(self, tokens, tag, length):
+        n = min(len(tokens), length, self.budget)
+        key = tuple(tokens[:n])
+        if key in self.keys:
+            i = self.keys.index(key)
+            del self.keys[i], self.tags[i]
+        self.keys.append(key)
+        self.tags.append(tag)
+        while sum(map(len, self.keys)) > self.budget:
+            del self.keys[0], self.tags[0]
+
+
+@pytest.mark.parametrize("block", [1, 3, 16, 128])
+def test_block_index_agrees_with_a_linear_scan(block):
+    """Random prompt families (shared stems, branches inside and at block
+    edges, exact repeats, prompts longer than the budget) through a random
+    mix of put/get/evict: the block-indexed cache returns the same match
+    length and the same entry as the linear scan, holds the same keys in
+    the same LRU order and releases exactly the entries it drops."""
+    import random
+
+    rng = random.Random(block)
+    stems = [[rng.randrange(6) for _ in range(rng.randrange(1, 300))] for _ in range(5)]
+
+    def prompt():
+        s = rng.choice(stems)
+        cut = rng.randrange(len(s) + 1)
+        tail = [rng.randrange(6) for _ in range(rng.randrange(0, 200))]
+        return s[:cut] + tail or [1]
+
+    for budget in (0, 50, 700, 5000):
+        cache, scan = PrefixCache(budget, block_tokens=block), _LinearScan(budget)
+        _Stored.released = []
+        live, stored = set(), set()
+        for step in range(400):
+            op = rng.random()
+            if op < 0.45:
+                p = prompt()
+                length = rng.randrange(1, len(p) + 2)
+                cache.put(p, _Stored(step, length))
+                if budget > 0:
+                    scan.put(p, step, length)
+                    stored.add(step)
+            elif op < 0.95:
+                p = prompt()
+                limit = rng.choice([None, rng.randrange(0, len(p) + 3)])
+                got = cache.get(p, max_prefix_len=limit)
+                want_len, want_tag = scan.get(p, limit) if budget else (0, None)
+                assert got.length == want_len, (step, got.length, want_len)
+                assert (got.cache.tag if got.cache else None) == want_tag
+                if got.cache is not None:
+                    assert got.cache.length == want_len
+            elif budget and scan.keys:
+                assert cache.evict_lru()
+                del scan.keys[0], scan.tags[0]
+            assert len(cache) == len(scan.keys) or budget == 0
+            assert cache.total_tokens == sum(map(len, scan.keys)) or budget == 0
+            live = set(scan.tags) if budget else set()
+        assert [e.cache.tag for e in cache._lru.values()] == list(live and scan.tags)
+        released = set(_Stored.released)
+        assert not released & live and released == stored - live
+        cache.clear()
+        assert len(cache) == 0 and cache.total_tokens == 0
+        assert not cache._root.next and not cache._root.tails and not cache._root.through
