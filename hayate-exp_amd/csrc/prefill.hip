@@ -72,6 +72,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRows = kPrefillRows;  // (token, head) rows per workgroup
 constexpr int kThreads = 2 * kRows;  // one wave per 32 rows
 constexpr float kLazy = 8.0f;  // rescale threshold, exp2 domain
+constexpr float kLazyP = 256.0f;  // 2^kLazy
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -336,10 +337,14 @@ void prefill_kernel(
   // row c's scores for keys 8 (i / 4) + 4 h + i % 4 of the block.
   // probs(): the common case, straight-line code the scheduler can
   // interleave with the next block's QK^T MFMAs: probabilities against the
-  // current base, packed to bf16, their sum and the row max. rebase(): when
-  // some row's max exceeds the base by more than kLazy (or a row sees its
-  // first key) the base moves and the block's probabilities are redone
-  // (rare).
+  // current base, packed to bf16, and their sum (pairwise tree: four
+  // dependent steps instead of fifteen). rebase(): when some row's
+  // max exceeds the base by more than kLazy (or a row sees its first key)
+  // the base moves and the block's probabilities are redone (rare). The
+  // row max is only computed when a lane's probabilities sum to more than
+  // 2^kLazy: below that no score of the lane can exceed the base by more
+  // than kLazy (each probability is at most the sum), so the common path
+  // carries no max tree.
   auto mask = [&](f32x16 &s, int kb0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -347,53 +352,55 @@ void prefill_kernel(
       s[i] = key > limit ? -INFINITY : s[i];
     }
   };
-  // Sums and maxima of a lane's 16 values are pairwise trees: four
-  // dependent steps instead of fifteen.
-  auto probs = [&](const f32x16 &s, bf16x8 &pop0, bf16x8 &pop1, float &psum, float &mx)
+  auto probs = [&](const f32x16 &s, bf16x8 &pop0, bf16x8 &pop1, float &psum)
                    __attribute__((always_inline)) {
-    float p[16];
+    float pp[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      p[i] = __builtin_amdgcn_exp2f(s[i]);
+      const float p = __builtin_amdgcn_exp2f(s[i]);
+      pp[i] = p;
       if (i < 8)
-        pop0[i] = static_cast<__bf16>(p[i]);
+        pop0[i] = static_cast<__bf16>(p);
       else
-        pop1[i - 8] = static_cast<__bf16>(p[i]);
+        pop1[i - 8] = static_cast<__bf16>(p);
     }
-    psum = tree_sum16(p);
-    mx = tree_max16(s);
+    psum = tree_sum16(pp);
   };
-  auto rebase = [&](const f32x16 &s, float mx, bf16x8 &pop0, bf16x8 &pop1, float &psum)
+  auto rebase = [&](const f32x16 &s, bf16x8 &pop0, bf16x8 &pop1, float &psum)
                     __attribute__((always_inline)) {
-    mx = halves_max(mx);  // row max relative to r_mma
-    const bool need = base == -INFINITY ? mx != -INFINITY : mx > kLazy;
-    if (__builtin_expect(__any(need), 0)) {
-      const float r_new = need ? mx + r_mma : r_mma;
-      const float delta = r_new - r_mma;
-      const float alpha = base == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(-delta);
-      if (need) {
-        base = r_new;
-        r_mma = r_new;
-      }
-      l_run *= alpha;
+    // !(psum <= ...) also catches an overflowed (infinite) sum
+    const bool check = base == -INFINITY || !(psum <= kLazyP);
+    if (__builtin_expect(__any(check), 0)) {
+      const float mx = halves_max(tree_max16(s));  // row max relative to r_mma
+      const bool need = base == -INFINITY ? mx != -INFINITY : mx > kLazy;
+      if (__any(need)) {
+        const float r_new = need ? mx + r_mma : r_mma;
+        const float delta = r_new - r_mma;
+        const float alpha = base == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(-delta);
+        if (need) {
+          base = r_new;
+          r_mma = r_new;
+        }
+        l_run *= alpha;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-      float p[16];
+        for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+        float pp[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(s[i] - delta);
-        if (i < 8)
-          pop0[i] = static_cast<__bf16>(p[i]);
-        else
-          pop1[i - 8] = static_cast<__bf16>(p[i]);
+        for (int i = 0; i < 16; ++i) {
+          pp[i] = __builtin_amdgcn_exp2f(s[i] - delta);
+          if (i < 8)
+            pop0[i] = static_cast<__bf16>(pp[i]);
+          else
+            pop1[i - 8] = static_cast<__bf16>(pp[i]);
+        }
+        psum = tree_sum16(pp);
+        const float hi = __uint_as_float(f32_to_bf16_rne(r_mma) << 16);
+        const float mid = __uint_as_float(f32_to_bf16_rne(r_mma - hi) << 16);
+        const float lo = r_mma - hi - mid;  // at most 8 significant bits left
+        shift_b[0] = static_cast<__bf16>(h == 0 ? -hi : 0.0f);
+        shift_b[1] = static_cast<__bf16>(h == 0 ? -mid : 0.0f);
+        shift_b[2] = static_cast<__bf16>(h == 0 ? -lo : 0.0f);
       }
-      psum = tree_sum16(p);
-      const float hi = __uint_as_float(f32_to_bf16_rne(r_mma) << 16);
-      const float mid = __uint_as_float(f32_to_bf16_rne(r_mma - hi) << 16);
-      const float lo = r_mma - hi - mid;  // at most 8 significant bits left
-      shift_b[0] = static_cast<__bf16>(h == 0 ? -hi : 0.0f);
-      shift_b[1] = static_cast<__bf16>(h == 0 ? -mid : 0.0f);
-      shift_b[2] = static_cast<__bf16>(h == 0 ? -lo : 0.0f);
     }
     l_run += psum;
   };
@@ -429,7 +436,7 @@ void prefill_kernel(
   f32x16 s_a, s_b;
   auto body = [&](bool masked, int j, f32x16 &s_cur, f32x16 &s_nxt) __attribute__((always_inline)) {
     bf16x8 pop0, pop1;
-    float psum, mx;
+    float psum;
     if (masked) mask(s_cur, kv_begin + 32 * j);  // blocks on the diagonal
     read_v(j, 0);
     __builtin_amdgcn_sched_barrier(0);
@@ -441,7 +448,7 @@ void prefill_kernel(
     __builtin_amdgcn_s_setprio(1);
     s_nxt = qk();
     read_v(j, 1);
-    probs(s_cur, pop0, pop1, psum, mx);
+    probs(s_cur, pop0, pop1, psum);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
@@ -453,7 +460,7 @@ void prefill_kernel(
     __asm__ volatile("" ::"v"(psum), "v"(pop0), "v"(pop1));
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(0);
-    rebase(s_cur, mx, pop0, pop1, psum);
+    rebase(s_cur, pop0, pop1, psum);
     s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_nxt, 0, 0, 0);
     read_k(j + 2);
     pv(pop0, pop1);
