@@ -442,7 +442,8 @@ extern "C" int hy_plan_tick(const int32_t *q_lens, const int32_t *kv_lens,
     pt[3] = p.kv0;
     pt[4] = p.kv1;
     pt[5] = p.slot;
-    pt[6] = pt[7] = 0;
+    pt[6] = q_begin[p.seq];
+    pt[7] = kv_lens[p.seq] - q_lens[p.seq];  // cached keys before the chunk
   }
   counts_out[0] = n_dec;
   counts_out[1] = n_merge;

@@ -165,7 +165,6 @@ void prefill_kernel(
     uint16_t *__restrict__ out, int64_t o_ss, int64_t o_st, int64_t o_sh,
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
     int64_t pool_hs, const int32_t *__restrict__ page_table, int64_t pt_stride,
-    const int32_t *__restrict__ q_start, const int32_t *__restrict__ kv_lens,
     const int32_t *__restrict__ items, float *__restrict__ ws_acc, float *__restrict__ ws_ml,
     int num_kv_heads, int page_shift, float scale_log2) {
   static_assert(kThreads == 512, "eight waves");
@@ -179,10 +178,12 @@ void prefill_kernel(
   const int kv_begin = it[3];
   const int kv_end = it[4];
   const int slot = it[5];
+  // the sequence's packed query row and cached length travel in the item,
+  // so the Q loads and page-table reads issue one dependent read after
+  // the kernel starts
+  const int qs = it[6];
+  const int cache_len = it[7];
   const int h0 = kvh * G;
-  const int qs = q_start[seq];
-  const int q_len = q_start[seq + 1] - qs;
-  const int cache_len = kv_lens[seq] - q_len;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -266,13 +267,17 @@ void prefill_kernel(
   // (pages hold >= 32 keys), so each tensor needs one page id per tile;
   // they are fetched a tile ahead. Rows at or past kv_end load the last
   // valid key (any finite data: their scores are masked).
+  // Page ids are non-negative (the host rejects others); held unsigned, they
+  // widen to 64 bits without a sign extension that would make the compiler
+  // wait for each id as soon as it is read. Keys are clamped to
+  // [0, last_key], so every read stays inside the sequence's row.
   struct Pages {
-    int32_t k, v;
+    uint32_t k, v;
   };
   auto fetch_pages = [&](int kt) __attribute__((always_inline)) {
     Pages pg;
-    pg.k = pt[min(kt + 16 * (wave >> 1), last_key) >> page_shift];
-    pg.v = pt[min(kt + 8 * wave, last_key) >> page_shift];
+    pg.k = static_cast<uint32_t>(pt[max(min(kt + 16 * (wave >> 1), last_key), 0) >> page_shift]);
+    pg.v = static_cast<uint32_t>(pt[max(min(kt + 8 * wave, last_key), 0) >> page_shift]);
     return pg;
   };
   auto issue_tile = [&](int kt, const Pages &pg, uint16_t *dst) __attribute__((always_inline)) {
@@ -466,12 +471,16 @@ void prefill_kernel(
     pv(pop0, pop1);
   };
 
-  // Prologue: tiles 0 and 1 in flight, then block 0's scores and block 1's
+  // Prologue: the page ids of tiles 0-2 are read together (one round trip:
+  // the tile loads below are inline assembly that no load may cross, so
+  // reads placed after the first tile's loads would each wait for their
+  // own), tiles 0 and 1 go in flight, then block 0's scores and block 1's
   // K operands.
-  if (n_tiles > 0) issue_tile(kv_begin, fetch_pages(kv_begin), smem);
-  if (n_tiles > 1) issue_tile(kv_begin + kTile, fetch_pages(kv_begin + kTile), smem + kStage);
-  Pages pg_next = {};
-  if (n_tiles > 2) pg_next = fetch_pages(kv_begin + 2 * kTile);
+  const Pages pg0 = fetch_pages(kv_begin);
+  const Pages pg1 = fetch_pages(kv_begin + kTile);
+  Pages pg_next = fetch_pages(kv_begin + 2 * kTile);
+  if (n_tiles > 0) issue_tile(kv_begin, pg0, smem);
+  if (n_tiles > 1) issue_tile(kv_begin + kTile, pg1, smem + kStage);
   wait_tile_loads();
   __syncthreads();
   read_k(0);
@@ -613,13 +622,12 @@ void launch_prefill(hipStream_t st, int num_kv_heads, int n_items, const uint16_
                     int64_t q_ss, int64_t q_st, int64_t q_sh, uint16_t *out, int64_t o_ss,
                     int64_t o_st, int64_t o_sh, const uint16_t *k_pool, const uint16_t *v_pool,
                     int64_t pool_hs, const int32_t *page_table, int64_t pt_stride,
-                    const int32_t *q_start, const int32_t *kv_lens, const int32_t *items,
-                    float *ws_acc, float *ws_ml, int page_shift, float scale_log2) {
+                    const int32_t *items, float *ws_acc, float *ws_ml, int page_shift,
+                    float scale_log2) {
   hipLaunchKernelGGL((prefill_kernel<G>), dim3(num_kv_heads, n_items), dim3(kThreads), 0,
                      st, q, q_ss,
                      q_st, q_sh, out, o_ss, o_st, o_sh, k_pool, v_pool, pool_hs, page_table,
-                     pt_stride, q_start, kv_lens, items, ws_acc, ws_ml, num_kv_heads, page_shift,
-                     scale_log2);
+                     pt_stride, items, ws_acc, ws_ml, num_kv_heads, page_shift, scale_log2);
 }
 
 template <int G>
@@ -696,8 +704,8 @@ extern "C" int hy_paged_prefill(
   case GG:                                                                                    \
     hy::launch_prefill<GG>(st, num_kv_heads, n_prefill, qq, q_stride_seq, q_stride_tok,       \
                            q_stride_head, oo, o_stride_seq, o_stride_tok, o_stride_head, kp,  \
-                           vp, pool_head_stride, page_table, page_table_stride, q_start,      \
-                           kv_lens, prefill_items, ws_acc, ws_ml, page_shift, scale_log2);    \
+                           vp, pool_head_stride, page_table, page_table_stride,               \
+                           prefill_items, ws_acc, ws_ml, page_shift, scale_log2);             \
     break;
   switch (G) {
     HY_PREFILL_CASE(1)

@@ -143,10 +143,11 @@ int hy_page_scatter(void *pool, int64_t pool_layer_stride,
  *   merge items   int32[n][4] = {seq, first_slot, num_partials, q_row}, one
  *                 per decode sequence (all of its pieces' partials);
  *   prefill items (q_len > 1): int32[n][8] =
- *                 {seq, q_begin, q_end, kv_begin, kv_end, slot, 0, 0}:
- *                 query tiles of 256 / G tokens, each over one range of keys
- *                 (kv_begin a multiple of 64), most keys first; slot as for
- *                 decode items;
+ *                 {seq, q_begin, q_end, kv_begin, kv_end, slot, q_row,
+ *                 cache_len}: query tiles of 256 / G tokens, each over one
+ *                 range of keys (kv_begin a multiple of 64), most keys
+ *                 first; slot as for decode items, q_row as for decode
+ *                 pieces, cache_len = kv_len - q_len of the sequence;
  *   prefill merge items int32[n][8] =
  *                 {seq, q_begin, q_end, first_slot, num_splits, q_row, 0, 0}.
  * Decode uses one chunk per CU and kv head (num_cus / num_kv_heads chunks,

@@ -150,8 +150,9 @@ def test_plan_chunk_cut_rounds_to_32_tokens():
 
 def check_prefill_cover(q, kv, p):
     """Every query tile's key range [0, cache + q1) is covered once by its
-    parts, which start on 64-key steps and are dispatched longest first; a
-    split tile has one merge item over its parts' partial slots."""
+    parts, which start on 64-key steps, carry the sequence's query row and
+    cached length, and are dispatched longest first; a split tile has one
+    merge item over its parts' partial slots."""
     pre = p.prefill
     tile = _native.lib().hy_prefill_tile_rows() // 4
     lengths = pre[:, 4] - pre[:, 3]
@@ -170,6 +171,8 @@ def check_prefill_cover(q, kv, p):
             parts = rows[(rows[:, 1] == q0)]
             n_parts += len(parts)
             assert (parts[:, 2] == q1).all()
+            assert (parts[:, 6] == sum(q[:s_])).all()  # packed query row of the sequence
+            assert (parts[:, 7] == cache).all()  # cached keys before the chunk
             parts = parts[np.argsort(parts[:, 3])]
             assert parts[0, 3] == 0 and parts[-1, 4] == cache + q1
             assert (parts[1:, 3] == parts[:-1, 4]).all() and (parts[:, 4] > parts[:, 3]).all()
