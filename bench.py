@@ -228,8 +228,10 @@ def engine_benchmark():
     engine, via hayate_amd.benchmark: prompt prefill of 512-token prompts
     and 64 decode steps, median of 3 after a warm-up, at batch 1 (the CLI's
     default) and batch 20 (the engine's default batch limit); synthetic
-    Qwen3-4B weights; eager, then with decode ticks replayed from captured
-    HIP graphs (Engine(compile=True))."""
+    Qwen3-4B weights; eager, then with ticks replayed from captured HIP
+    graphs (Engine(compile=True): decode shapes from their first tick,
+    prompt shapes from their second, so the warm-up run's prompt tick
+    runs eagerly and the first timed one is captured)."""
     from hayate_amd import benchmark
     from hayate_amd.engine import Engine
     from hayate_amd.model import Qwen3Config
@@ -240,7 +242,7 @@ def engine_benchmark():
         for b in (1, 20):
             rows = benchmark.run(eng, batch_size=b, context_tokens=512, decode_steps=64,
                                  repetitions=3)
-            key = f"batch_{b}" + ("_decode_graphs" if compiled else "")
+            key = f"batch_{b}" + ("_graphs" if compiled else "")
             out[key] = [{k: (round(v, 3) if isinstance(v, float) else v)
                          for k, v in r.items()} for r in rows]
         del eng

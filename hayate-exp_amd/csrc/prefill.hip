@@ -184,6 +184,8 @@ void prefill_kernel(
   const int qs = it[6];
   const int cache_len = it[7];
   const int h0 = kvh * G;
+  // an empty record (q_end <= q_begin) pads a list to a fixed launch size
+  if (q_end <= q_begin) return;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -566,6 +568,8 @@ __global__ __launch_bounds__(512) void prefill_merge_kernel(
   const int q_end = it0.z;
   const int first = it0.w;
   const int nsplit = it1.x;
+  // an empty record pads a list to a fixed launch size
+  if (q_end <= q_begin || nsplit <= 0) return;
   const int r = 32 * blockIdx.z + (threadIdx.x >> 4);
   const int d = (threadIdx.x & 15) * 8;
   const int i = q_begin + r / G;

@@ -158,7 +158,7 @@ class TickPlan:
         self.n_chunks = n_chunks
         self.merge = merge                  # int32 (n, 4) {seq, first_slot, num_partials, q_row}
         self.n_slots = n_slots
-        self.prefill = prefill              # int32 (n, 8) {seq, q0, q1, kv0, kv1, slot, 0, 0}
+        self.prefill = prefill              # int32 (n, 8) {seq, q0, q1, kv0, kv1, slot, q_row, cache}
         self.prefill_merge = prefill_merge  # int32 (n, 8) {seq, q0, q1, first_slot, splits, q_row, ..}
         self.n_prefill_slots = n_prefill_slots
 

@@ -19,7 +19,7 @@ every request produces its full token count.
 
 Run as ``python -m hayate_amd.benchmark [--model DIR] --batch-size B
 --context-tokens N --decode-steps S [--compile]``; without --model the
-engine uses synthetic Qwen3-4B weights; --compile replays decode ticks from
+engine uses synthetic Qwen3-4B weights; --compile replays ticks from
 captured HIP graphs (the reference's CLI flag of the same name compiles
 with torch.compile).
 """
@@ -175,7 +175,7 @@ def main(argv: Optional[List[str]] = None) -> List[dict]:
     ap.add_argument("--decode-steps", type=_positive, default=64)
     ap.add_argument("--repetitions", type=_positive, default=3)
     ap.add_argument("--compile", action="store_true",
-                    help="replay decode ticks from captured HIP graphs")
+                    help="replay ticks from captured HIP graphs")
     ap.add_argument("--compile-mode", default="default")
     ap.add_argument("--max-cache-tokens", type=_positive, default=None,
                     help="pool size (default: enough for the batch, at least the engine's)")

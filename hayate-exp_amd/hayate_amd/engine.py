@@ -41,11 +41,11 @@ from .constants import (
     DEFAULT_PREFILL_CHUNK_SIZE,
     MAX_BATCH_SIZE,
 )
-from .decode_graph import DecodeGraphRunner
 from .model import Qwen3Config, Qwen3Model, init_synthetic_weights, load_local_weights
 from .paged_cache import PagedCacheHandle, PagedKVCacheManager, PagedPrefix
 from .prefix_cache import PrefixCache
 from .sampler import Sampler
+from .tick_graph import TickGraphRunner
 
 DEFAULT_PREFIX_CACHE_MAX_TOKENS = 4096  # constants.py:27
 
@@ -120,10 +120,11 @@ class Engine:
         device: str = "cuda",
     ):
         """Positional arguments follow the reference's Engine (engine.py:29-39).
-        compile=True replays decode ticks from captured HIP graphs
-        (decode_graph.py) — except in "max-autotune-no-cudagraphs" mode,
-        which by its name asks for no graphs; there is no torch.compile on
-        this path."""
+        compile=True replays ticks from captured HIP graphs (tick_graph.py):
+        decode ticks from their first occurrence, ticks with prompt chunks
+        from the second occurrence of their shape on — except in
+        "max-autotune-no-cudagraphs" mode, which by its name asks for no
+        graphs; there is no torch.compile on this path."""
         if not torch.cuda.is_available():
             raise RuntimeError("the engine needs a HIP GPU")
         if compile_mode not in COMPILE_MODES:
@@ -171,8 +172,8 @@ class Engine:
             num_q_heads=self.model.num_heads,
         )
         self.last_tick = TickStats()
-        self.decode_graphs = (
-            DecodeGraphRunner(self.model, self.paged_cache, self.max_position_embeddings)
+        self.tick_graphs = (
+            TickGraphRunner(self.model, self.paged_cache, self.max_position_embeddings)
             if compile and compile_mode != "max-autotune-no-cudagraphs" else None
         )
 
@@ -298,9 +299,9 @@ class Engine:
             q_lens.append(len(chunk))
             tokens.extend(chunk)
         logits = None
-        if self.decode_graphs is not None and all(q == 1 for q in q_lens):
+        if self.tick_graphs is not None:
             self._reserve_tick(handles, q_lens)
-            logits = self.decode_graphs.run(handles, tokens)
+            logits = self.tick_graphs.run(handles, q_lens, tokens)
         if logits is None:
             paged = self._begin_tick(handles, q_lens)
             ids = torch.tensor(tokens, dtype=torch.long, device=self.device).unsqueeze(0)

@@ -216,9 +216,10 @@ def test_benchmark_reports_prefill_and_decode():
 
 def test_compiled_engine_replays_decode_graphs_like_eager():
     """Engine(compile=True) replays decode ticks from captured HIP graphs
-    (decode_graph.py). Over ticks that cross page boundaries, with the
+    (tick_graph.py). Over ticks that cross page boundaries, with the
     batch shrinking as requests finish (3, then 2, then 1 sequences: one
-    capture per batch size), the greedy tokens equal the eager engine's."""
+    capture per batch size; the one prompt tick's shape occurs once and
+    runs eagerly), the greedy tokens equal the eager engine's."""
     say("[engine: decode graphs against eager]")
     lengths, max_tokens = (120, 250, 40), (12, 30, 8)
     prompts = [prompt(40 + i, n) for i, n in enumerate(lengths)]
@@ -235,8 +236,8 @@ def test_compiled_engine_replays_decode_graphs_like_eager():
 
     eager, t_eager = run(False)
     graphs, t_graph = run(True)
-    assert eager.decode_graphs is None
-    runner = graphs.decode_graphs
+    assert eager.tick_graphs is None
+    runner = graphs.tick_graphs
     say(f"  captures {runner.captures}, replays {runner.replays}")
     # one capture per batch size, although the plan's chunk count changes
     # every 64 tokens of total context at these lengths
@@ -279,8 +280,51 @@ def test_compiled_engine_with_prefix_cache_and_admission_matches_eager():
 
     _, t_eager, hits_eager = run(False)
     eng, t_graph, hits_graph = run(True)
-    say(f"  prefix hits {hits_graph}, captures {eng.decode_graphs.captures}, "
-        f"replays {eng.decode_graphs.replays}")
+    say(f"  prefix hits {hits_graph}, captures {eng.tick_graphs.captures}, "
+        f"replays {eng.tick_graphs.replays} ({eng.tick_graphs.prompt_replays} with prompt chunks)")
     assert hits_eager == hits_graph >= 3
-    assert eng.decode_graphs.replays > 0
+    assert eng.tick_graphs.replays > 0
     assert t_graph == t_eager
+
+
+def test_compiled_engine_replays_prompt_and_mixed_ticks_like_eager():
+    """Ticks with prompt chunks replayed from graphs: three prompts of
+    1,300, 1,300 and 700 tokens in 256-token chunks give the shapes
+    (256, 256, 256) twice, (256, 256, 188), then (256, 256, 1) twice (the
+    third request decodes while the others prefill) and decode ticks. A
+    prompt shape is captured on its second occurrence, at a larger cached
+    length than the first, so its plan differs (more split query tiles;
+    the padded item lists carry other real counts). The greedy tokens
+    equal the eager engine's, and so do both pools bit for bit at the end:
+    every layer's appended K/V rows of every tick, replayed or not."""
+    say("[engine: prompt and mixed ticks from graphs against eager]")
+    lengths, max_tokens = (1300, 1300, 700), (6, 5, 9)
+    prompts = [prompt(70 + i, n) for i, n in enumerate(lengths)]
+
+    def run(compiled):
+        eng = make_engine(compile=compiled, prefill_chunk_size=256)
+        reqs = [Request(id=i, prompt_tokens=list(p), max_tokens=m)
+                for i, (p, m) in enumerate(zip(prompts, max_tokens))]
+        for r in reqs:
+            eng.add_request(r)
+        sizes = []
+        while eng.generate():
+            sizes.append((eng.last_tick.prefill_tokens, eng.last_tick.decode_tokens))
+        torch.cuda.synchronize()
+        return eng, [r.tokens for r in reqs], sizes
+
+    eager, t_eager, s_eager = run(False)
+    eng, t_graph, s_graph = run(True)
+    runner = eng.tick_graphs
+    say(f"  ticks (prefill, decode tokens): {s_graph}")
+    say(f"  captures {runner.captures}, replays {runner.replays}, "
+        f"with prompt chunks {runner.prompt_replays}")
+    assert s_graph == s_eager
+    assert s_graph[:5] == [(768, 0), (768, 0), (700, 0), (512, 1), (512, 1)]
+    assert t_graph == t_eager
+    assert runner.prompt_replays >= 2
+    for name in ("k_cache", "v_cache"):
+        a = getattr(eager.paged_cache, name).view(torch.int16)
+        b = getattr(eng.paged_cache, name).view(torch.int16)
+        assert torch.equal(a, b), f"{name} differs between the eager and the replayed engine"
+    assert eng.paged_cache.free_page_count == eng.paged_cache.num_pages

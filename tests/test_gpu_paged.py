@@ -633,3 +633,85 @@ def test_few_key_rows_exact_base():
     err = np.abs(got[rows] - e)
     say(f"  max_abs {err.max():.4f}")
     assert err.max() <= 0.011, err.max()
+
+
+def test_static_tick_batch_replays_one_shape_at_other_lengths():
+    """A mixed tick shape (two prompt chunks, three decode tokens) captured
+    once over a StaticTickBatch (tick_graph.py: fixed metadata buffers,
+    decode chunk and prefill item lists padded with empty records) and
+    replayed at two sets of cached lengths whose plans differ (other
+    prefill item, split and decode chunk counts): each replay, after an
+    in-place refresh, equals an eager begin_tick batch at the same lengths
+    bit for bit (rotated q, pools, attention), and the second matches the
+    oracle."""
+    from hayate_amd.tick_graph import StaticTickBatch
+
+    say("[static tick batch: one capture, two plans]")
+    q_lens = [256, 320, 1, 1, 1]
+    lens_a = [0, 1024, 100, 300, 37]
+    lens_b = [256, 3500, 1500, 2001, 38]
+    w = _custom_workload(32, 8, lens_b, q_lens, seed=11)
+    m, hs = w.manager, w.handles
+    pre = (m.k_cache.clone(), m.v_cache.clone())
+
+    def set_lengths(lens):
+        for h, c in zip(hs, lens):
+            h.length = c
+        m.k_cache.copy_(pre[0])
+        m.v_cache.copy_(pre[1])
+
+    def step(batch):
+        q_rot = batch.norm_rope_write_layer(0, w.q, w.k, w.v, w.q_norm_w, w.k_norm_w, EPS,
+                                            w.cos, w.sin)
+        return q_rot, batch.attend_layer(q_rot, 0)
+
+    plans = []
+    expected = []
+    for lens in (lens_a, lens_b):
+        set_lengths(lens)
+        eager = PagedKVBatch(m, q_lens, list(lens), [list(h.pages) for h in hs], varlen=True,
+                             num_q_heads=32)
+        plans.append(eager.plan(32).host)
+        q_e, o_e = step(eager)
+        torch.cuda.synchronize()
+        expected.append((bits(q_e), bits(o_e), layer_bits(m)))
+    say(f"  prefill items {[len(p.prefill) for p in plans]}, "
+        f"slots {[p.n_prefill_slots for p in plans]}, chunks {[p.n_chunks for p in plans]}")
+    assert len(plans[0].prefill) != len(plans[1].prefill)
+    assert plans[0].n_chunks != plans[1].n_chunks
+
+    slots = max(p.n_prefill_slots for p in plans) + 4
+    static = StaticTickBatch(m, q_lens, 32, max_tokens=max(c + q for c, q in zip(lens_b, q_lens)),
+                             prefill_slots=slots)
+    set_lengths(lens_a)
+    assert static.refresh(hs)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(static)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        q_g, o_g = step(static)
+    for rep, (lens, (q_e, o_e, pools_e)) in enumerate(zip((lens_a, lens_b, lens_a),
+                                                         expected + expected[:1])):
+        set_lengths(lens)
+        assert static.refresh(hs)
+        q_g.zero_()
+        o_g.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(q_g), q_e), f"replay {rep}: rotated q differs"
+        assert np.array_equal(bits(o_g), o_e), f"replay {rep}: attention differs"
+        k_b, v_b = layer_bits(m)
+        assert np.array_equal(k_b, pools_e[0]) and np.array_equal(v_b, pools_e[1]), \
+            f"replay {rep}: pools differ"
+    # the second length set against the oracle
+    set_lengths(lens_b)
+    pre_k, pre_v = layer_bits(m)
+    w.cache_lens = list(lens_b)
+    pk, pv, q_exp, o_exp = oracle_step(w, pre_k, pre_v)
+    q_e, o_e, pools_e = expected[1]
+    assert np.array_equal(q_e, q_exp) and np.array_equal(pools_e[0], pk)
+    assert_attention_close(o_e, o_exp, "static tick, second lengths")
