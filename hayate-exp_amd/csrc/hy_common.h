@@ -102,17 +102,41 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
-// Sequence index owning packed token `tok` given cumulative q_start[0..n].
-__device__ __forceinline__ int find_seq(const int32_t *q_start, int num_seqs, int tok) {
-  int lo = 0, hi = num_seqs - 1;
-  while (lo < hi) {
-    int mid = (lo + hi + 1) >> 1;
-    if (q_start[mid] <= tok)
-      lo = mid;
-    else
-      hi = mid - 1;
+// Sequence and position of packed token `tok`: the sequence is the last
+// index b with q_start[b] <= tok (cumulative query lengths q_start[0..n]),
+// the position cache_lens[b] + tok - q_start[b]. tok is wave-uniform and
+// below q_start[num_seqs]; every lane of the wave must be active (the
+// search spreads candidates over the 64 lanes and reads the result with a
+// ballot). Each round narrows [lo, lo + n) to one of 64 buckets with one
+// vector load, so up to 64 sequences take a single round trip, where a
+// binary search on scalar loads waits for log2(num_seqs) dependent ones.
+// Indexes are clamped into [lo, lo + n), so every load stays in bounds.
+struct TokenPos {
+  int seq, pos;
+};
+__device__ __forceinline__ TokenPos locate_token(const int32_t *__restrict__ q_start,
+                                                 const int32_t *__restrict__ cache_lens,
+                                                 int num_seqs, int tok) {
+  const int lane = static_cast<int>(threadIdx.x & (kWave - 1));
+  int lo = 0, n = num_seqs;  // q_start[lo] <= tok < q_start[lo + n]
+  while (n > kWave) {
+    const int step = (n + kWave - 1) / kWave;
+    const int idx = lo + lane * step;
+    const bool ok = idx < lo + n && q_start[min(idx, lo + n - 1)] <= tok;
+    const uint64_t m = __ballot(ok);  // lane 0 (idx = lo) always holds
+    const int j = 63 - __clzll(static_cast<long long>(m));
+    const int nlo = lo + j * step;
+    n = min(step, lo + n - nlo);
+    lo = nlo;
   }
-  return lo;
+  const int idx = lo + min(lane, n - 1);
+  const int qs = q_start[idx];
+  const int cl = cache_lens[idx];
+  const uint64_t m = __ballot(lane < n && qs <= tok);
+  const int j = 63 - __clzll(static_cast<long long>(m));
+  const int q_row = __builtin_amdgcn_readlane(qs, j);
+  const int cache = __builtin_amdgcn_readlane(cl, j);
+  return {lo + j, cache + tok - q_row};
 }
 
 }  // namespace hy

@@ -5,7 +5,8 @@
 // (16 bytes), so a wave covers four head rows with fully coalesced 256-byte
 // row segments. The fused norm + rotation + append gives 8 lanes to a row
 // (two 128-byte halves per lane group; see qknorm.h). Both appends take one
-// token per wave and read its sequence, position and page with scalar loads.
+// token per wave; its sequence and position come from one wave-wide search
+// round (locate_token) and its page from a scalar load.
 //
 // Built with -ffp-contract=off: the norm and rotation must round each fp32
 // product and sum separately, as the reference's chain of elementwise torch
@@ -36,8 +37,9 @@ __device__ __forceinline__ int64_t phys_token(const int32_t *__restrict__ pt,
 // Plain append: pool[h, phys(b, c_b + i)] = src[b, i, h]  (K and V).
 // One token per wave and 8 kv heads per grid row (blockIdx.y): the wave's 16
 // rows (8 K, 8 V) go in four 16-lane row loads per lane. The token is
-// wave-uniform, so its sequence and page are scalar loads; without a
-// per-sequence stride the row loads are issued before them.
+// wave-uniform: its sequence and position take one search round and its
+// page a scalar load; without a per-sequence stride the row loads are
+// issued before them.
 // ---------------------------------------------------------------------------
 template <bool kSeqStride>
 __global__ __launch_bounds__(256) void kv_append_kernel(
@@ -66,10 +68,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     }
   };
   if (!kSeqStride) issue_loads(0);
-  const int b = find_seq(q_start, num_seqs, tok);
-  const int pos = cache_lens[b] + tok - q_start[b];
+  const TokenPos tp = locate_token(q_start, cache_lens, num_seqs, tok);
+  const int b = tp.seq;
   if (kSeqStride) issue_loads(b);
-  const int64_t p = phys_token(page_table, pt_stride, b, pos, page_size);
+  const int64_t p = phys_token(page_table, pt_stride, b, tp.pos, page_size);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 4 * j + grp;
@@ -88,8 +90,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 // V pool). Grid (token blocks of 4, ceil(Hq / 32) q chunks then
 // ceil(Hkv / 8) kv chunks). The token's sequence, position and page, the
 // norm weights and the cos/sin row are looked up once per wave; the token is
-// uniform over the wave, so the sequence search and the page lookup are
-// scalar loads, which retire on their own counter. Without a per-sequence
+// uniform over the wave, so the sequence and position take one wave-wide
+// search round and the page a scalar load. Without a per-sequence
 // stride (packed or contiguous batches) a row's address needs only the
 // token index, so the row loads are issued first and stay in flight through
 // the search.
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
   const int h0 = is_q ? blockIdx.y * kQChunk + slot : (blockIdx.y - gq) * kKvChunk + slot;
   const int nrows = is_q ? (h0 < num_q_heads ? min(kQRows, (num_q_heads - h0 + 7) / 8) : 0)
                          : (h0 < num_kv_heads ? 1 : 0);
-  const bool live = tok < total_tokens && nrows > 0;
+  const bool live = nrows > 0;
 
   // raw[2 j], raw[2 j + 1]: lo and hi halves of q row j; for kv: k then v.
   u32x4 raw[2 * kQRows];
@@ -155,21 +157,25 @@ __global__ __launch_bounds__(256) void qknorm_rope_append_kernel(
       raw[3] = load16(vs + 64);
     }
   };
-  // A whole 8-lane group leaves together, so the group's DPP reads below
-  // only see active lanes.
-  if (!live) return;
-  if (!kSeqStride) issue_loads(0);
+  if (tok >= total_tokens) return;  // the whole wave
+  if (!kSeqStride && live) issue_loads(0);
   // Every load is issued before the first use of any: rows, weights, the
-  // token's sequence (scalar), the cos/sin row and the page (scalar).
+  // token's sequence and position (one search round), the cos/sin row and
+  // the page (scalar).
   const uint16_t *w = is_q ? q_w : k_w;
   const float eps = is_q ? q_eps : k_eps;
   u32x4 w_lo, w_hi;
-  if (w != nullptr) {
+  if (live && w != nullptr) {
     w_lo = load16(w + lane * 8);
     w_hi = load16(w + 64 + lane * 8);
   }
-  const int b = find_seq(q_start, num_seqs, tok);
-  const int pos = cache_lens[b] + tok - q_start[b];
+  // every lane of the wave takes part in the search
+  const TokenPos tp = locate_token(q_start, cache_lens, num_seqs, tok);
+  // A whole 8-lane group leaves together, so the group's DPP reads below
+  // only see active lanes.
+  if (!live) return;
+  const int b = tp.seq;
+  const int pos = tp.pos;
   if (kSeqStride) issue_loads(b);
   const bool rot = cos_t != nullptr;
   float cl[8], ch[8], sl[8], sh[8];
