@@ -19,8 +19,10 @@
 //                 lane); B = Q^T held in registers. Lane (c, h) ends with
 //                 row c's scores for keys 8 (i / 4) + 4 h + i % 4, i < 16,
 //                 of the 32-key block.
-//   softmax       per row: the two lanes of a row differ only in h; the
-//                 row max and sum cross halves with v_permlane32_swap.
+//   softmax       per row: p = exp2(fma(s, scale * log2(e), -base)), the
+//                 score scaling in fp32 as the reference's; the two lanes
+//                 of a row differ only in h; the row max and sum cross
+//                 halves with v_permlane32_swap.
 //   O^T += V^T P^T  B = P^T: the first (last) eight of the lane's scores
 //                 are row c's probabilities for MFMA k index 8 h + j once k
 //                 stands for key 16 kh + (j < 4 ? 4 h + j : 8 + 4 h + j - 4);
@@ -212,11 +214,6 @@ void prefill_kernel(
       u32x4 w = raw[kk];
       if (!live) w = u32x4{0u, 0u, 0u, 0u};
       qop[kk] = __builtin_bit_cast(bf16x8, w);
-      // Scores come out of the MFMA in exp2 units: q * scale * log2(e),
-      // rounded to bf16 once here.
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        qop[kk][e] = static_cast<__bf16>(static_cast<float>(qop[kk][e]) * scale_log2);
     }
   }
 
@@ -225,23 +222,17 @@ void prefill_kernel(
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[db][i] = 0.f;
-  // Exponent base of this lane's row, in exp2 units (fp32); -inf until the
-  // row has seen a key. The QK^T chain subtracts it (as r_mma, 0 while
-  // unset) with one more MFMA: A = 1 in k indices 0-2 (a constant), B = the
-  // three bf16 parts of -r_mma (hi + mid + lo hold its 24 bits exactly) in
-  // k indices 0-2 of this row, so the scores come out shifted by the exact
-  // base and the probabilities are plain exp2 of them. With an exact base
-  // the row max's probability is exactly 1 when the base is set, so its
-  // bf16 rounding for the P V product matches the fp32 row sum.
+  // Scores come out of the MFMA unscaled (q and k as stored). A row's
+  // probabilities are exp2(fma(s, scale * log2(e), -shift)): the fp32 score
+  // scaling, in exp2 units, and the subtraction of the row's exponent base
+  // rounded once. base is that exponent base, -inf until the row has seen a
+  // key; shift is the value subtracted (0 while base is unset). The base is
+  // set to the rounded scaled row max, so the max's own argument is within
+  // an ulp of 0 and its probability rounds to 1 in bf16 for the P V product
+  // as in the fp32 row sum.
   float base = -INFINITY;
-  float r_mma = 0.f;
+  float shift = 0.f;
   float l_run = 0.f;
-  bf16x8 shift_a, shift_b;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    shift_a[e] = static_cast<__bf16>(e < 3 && h == 0 ? 1.0f : 0.0f);
-    shift_b[e] = static_cast<__bf16>(0.0f);
-  }
 
   // Causal limits: this row sees keys <= limit; every live row of the wave
   // sees keys <= wave_lo; no live row of the wave sees a key > wave_hi.
@@ -319,12 +310,10 @@ void prefill_kernel(
 
   // Software pipeline over this wave's blocks. Block j's body runs the
   // QK^T MFMAs of block j + 1 while the VALU does block j's softmax (the
-  // two are independent), then block j + 1's base shift, then block j's
-  // P V MFMAs; K operands are read two blocks ahead and V operands at the
-  // start of their block, so no LDS read is waited for right after it is
-  // issued. The scores a block's softmax sees were shifted by the base at
-  // the time of its QK^T, and the base only moves in the softmax (before
-  // the next shift), so scores and base always agree.
+  // two are independent), then block j's P V MFMAs; K operands are read
+  // two blocks ahead and V operands at the start of their block, so no LDS
+  // read is waited for right after it is issued. The scores are raw, so a
+  // block's softmax applies the base as it stands when the softmax runs.
   bf16x8 kop[8];
   auto read_k = [&](int j) __attribute__((always_inline)) {
     const uint16_t *kb = k_block(j);
@@ -340,8 +329,8 @@ void prefill_kernel(
     return s;
   };
 
-  // Softmax of one block's scores s (relative to r_mma): lane (c, h) holds
-  // row c's scores for keys 8 (i / 4) + 4 h + i % 4 of the block.
+  // Softmax of one block's raw scores s: lane (c, h) holds row c's scores
+  // for keys 8 (i / 4) + 4 h + i % 4 of the block.
   // probs(): the common case, straight-line code the scheduler can
   // interleave with the next block's QK^T MFMAs: probabilities against the
   // current base, packed to bf16, and their sum (pairwise tree: four
@@ -364,7 +353,7 @@ void prefill_kernel(
     float pp[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float p = __builtin_amdgcn_exp2f(s[i]);
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], scale_log2, -shift));
       pp[i] = p;
       if (i < 8)
         pop0[i] = static_cast<__bf16>(p);
@@ -378,15 +367,16 @@ void prefill_kernel(
     // !(psum <= ...) also catches an overflowed (infinite) sum
     const bool check = base == -INFINITY || !(psum <= kLazyP);
     if (__builtin_expect(__any(check), 0)) {
-      const float mx = halves_max(tree_max16(s));  // row max relative to r_mma
-      const bool need = base == -INFINITY ? mx != -INFINITY : mx > kLazy;
+      const float mraw = halves_max(tree_max16(s));  // raw row max
+      const float mx = __builtin_fmaf(mraw, scale_log2, -shift);  // relative to shift
+      const bool need = base == -INFINITY ? mraw != -INFINITY : mx > kLazy;
       if (__any(need)) {
-        const float r_new = need ? mx + r_mma : r_mma;
-        const float delta = r_new - r_mma;
+        const float s_new = need ? mraw * scale_log2 : shift;
+        const float delta = s_new - shift;
         const float alpha = base == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(-delta);
         if (need) {
-          base = r_new;
-          r_mma = r_new;
+          base = s_new;
+          shift = s_new;
         }
         l_run *= alpha;
 #pragma unroll
@@ -394,19 +384,13 @@ void prefill_kernel(
         float pp[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          pp[i] = __builtin_amdgcn_exp2f(s[i] - delta);
+          pp[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], scale_log2, -shift));
           if (i < 8)
             pop0[i] = static_cast<__bf16>(pp[i]);
           else
             pop1[i - 8] = static_cast<__bf16>(pp[i]);
         }
         psum = tree_sum16(pp);
-        const float hi = __uint_as_float(f32_to_bf16_rne(r_mma) << 16);
-        const float mid = __uint_as_float(f32_to_bf16_rne(r_mma - hi) << 16);
-        const float lo = r_mma - hi - mid;  // at most 8 significant bits left
-        shift_b[0] = static_cast<__bf16>(h == 0 ? -hi : 0.0f);
-        shift_b[1] = static_cast<__bf16>(h == 0 ? -mid : 0.0f);
-        shift_b[2] = static_cast<__bf16>(h == 0 ? -lo : 0.0f);
       }
     }
     l_run += psum;
@@ -437,9 +421,9 @@ void prefill_kernel(
   // holds at most 15 outstanding reads, so the first MFMA's wait for the K
   // operands cannot leave all 16 in flight); then QK^T of block j + 1 on the
   // matrix core, interleaved with the other V reads and block j's
-  // probabilities (one MFMA, one LDS read, six VALU instructions, eight
-  // times); then the rare rebase, block j + 1's base shift, the K reads of
-  // block j + 2 and block j's P V.
+  // probabilities (one MFMA, one LDS read, seven VALU instructions, eight
+  // times); then the rare rebase, the K reads of block j + 2 and block j's
+  // P V.
   f32x16 s_a, s_b;
   auto body = [&](bool masked, int j, f32x16 &s_cur, f32x16 &s_nxt) __attribute__((always_inline)) {
     bf16x8 pop0, pop1;
@@ -460,7 +444,7 @@ void prefill_kernel(
     for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedValu, 6, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 7, 0);
     }
     // the probabilities count as used here, so the compiler keeps them in
     // this straight-line region instead of sinking them past the rebase test
@@ -468,7 +452,6 @@ void prefill_kernel(
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(0);
     rebase(s_cur, pop0, pop1, psum);
-    s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_nxt, 0, 0, 0);
     read_k(j + 2);
     pv(pop0, pop1);
   };
@@ -487,7 +470,6 @@ void prefill_kernel(
   __syncthreads();
   read_k(0);
   s_a = qk();
-  s_a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(shift_a, shift_b, s_a, 0, 0, 0);
   read_k(1);
 
   // Tile t: tile t + 2's loads go into the stage tile t - 1 used (every wave

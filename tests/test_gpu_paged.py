@@ -715,3 +715,27 @@ def test_static_tick_batch_replays_one_shape_at_other_lengths():
     q_e, o_e, pools_e = expected[1]
     assert np.array_equal(q_e, q_exp) and np.array_equal(pools_e[0], pk)
     assert_attention_close(o_e, o_exp, "static tick, second lengths")
+
+
+def test_large_logits_scaled_in_fp32():
+    """Scores 16 times the unit-norm case (both q/k norm weights x 4, so a
+    row's scaled scores spread over tens of exp2 units and the softmax is
+    peaky), on a tick with two prompt chunks and three decode tokens. The
+    kernels scale scores in fp32 as the reference does; a query pre-scaled
+    and rounded to bf16 before the product (what the prefill kernel once
+    did) measured max-abs 0.14 and relative RMS 5.7e-3 here. Tolerance for
+    this case: relative RMS 5e-3, max-abs 4e-2 (outputs reach ~4 in
+    magnitude, where one bf16 step is 1.6e-2)."""
+    say("[large logits]")
+    for seed in (1, 2):
+        w = _custom_workload(32, 8, [0, 700, 1500, 300, 2000], [256, 200, 1, 1, 1], seed=seed)
+        w.q_norm_w = (w.q_norm_w.float() * 4).to(torch.bfloat16)
+        w.k_norm_w = (w.k_norm_w.float() * 4).to(torch.bfloat16)
+        pre_k, pre_v = layer_bits(w.manager)
+        q_rot, out = gpu_step(w)
+        post_k, post_v = layer_bits(w.manager)
+        pk, pv, q_exp, o_exp = oracle_step(w, pre_k, pre_v)
+        assert np.array_equal(bits(q_rot), q_exp) and np.array_equal(post_k, pk)
+        st = R.compare(bits(out), o_exp)
+        say(f"  seed {seed}: max_abs={st['max_abs']:.3e} rel_rms={st['rel_rms']:.3e}")
+        assert st["finite"] and st["rel_rms"] <= 5e-3 and st["max_abs"] <= 4e-2, st
