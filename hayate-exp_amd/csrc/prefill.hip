@@ -58,9 +58,10 @@
 // prefill_merge_kernel (hy_paged_prefill_merge) combines the splits of a
 // query tile afterwards.
 //
-// Item key ranges start at multiples of 32 keys (hy_plan_tick cuts at
-// multiples of the tile size), so each 32-key row group of a tile lies in
-// one page and its page-table entry is a scalar load.
+// Item key ranges start at multiples of 64 keys (hy_plan_tick cuts at
+// multiples of the 64-key tile), so the rows one wave loads of a tile lie
+// in one page (pages hold at least 32 keys) and their page-table entry is a
+// scalar load.
 
 #include <type_traits>
 
