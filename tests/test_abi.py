@@ -198,6 +198,28 @@ def test_plan_prefill_tiles_cover_every_query_and_key_once():
     assert len(check_prefill_cover(q, kv, p)) > 0
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_plan_list_sizes_fit_a_fixed_launch(seed):
+    """The bounds a replayed graph sizes its padded lists by
+    (hayate_amd/tick_graph.py): a plan has at most one decode chunk per CU
+    and kv head, at most one prefill item per unsplit query tile plus one per
+    partial slot, at most one prefill merge item per query tile, and one
+    decode merge item per decode sequence."""
+    rng = np.random.default_rng(300 + seed)
+    n = int(rng.integers(1, 20))
+    q = [1 if rng.random() < 0.5 else int(rng.integers(2, 1025)) for _ in range(n)]
+    kv = [x + int(rng.integers(0, 16000)) for x in q]
+    for cus in (64, 256):
+        p = plan(q, kv, cus=cus)
+        tile = _native.lib().hy_prefill_tile_rows() // 4
+        n_tiles = sum(-(-x // tile) for x in q if x > 1)
+        split_tiles = len(p.prefill_merge)
+        assert len(p.prefill) == (n_tiles - split_tiles) + p.n_prefill_slots
+        assert split_tiles <= n_tiles
+        assert p.n_chunks <= max(1, cus // 8)
+        assert len(p.merge) == sum(1 for x in q if x == 1)
+
+
 @pytest.mark.parametrize("shape", ["prefill_4x512", "mixed_tick", "random0", "random1", "random2"])
 def test_plan_prefill_cover_across_shapes(shape):
     """The split rules the planner picks from (even parts, or full parts of
