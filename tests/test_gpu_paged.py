@@ -739,3 +739,39 @@ def test_large_logits_scaled_in_fp32():
         st = R.compare(bits(out), o_exp)
         say(f"  seed {seed}: max_abs={st['max_abs']:.3e} rel_rms={st['rel_rms']:.3e}")
         assert st["finite"] and st["rel_rms"] <= 5e-3 and st["max_abs"] <= 4e-2, st
+
+
+def test_static_tick_batch_refuses_a_plan_past_its_slots():
+    """A StaticTickBatch sized for fewer prefill partial slots than a tick's
+    plan needs leaves its buffers alone, returns False and reports the
+    slots needed; a batch built with that many serves the tick, and its
+    (uncaptured) calls equal an eager batch's bit for bit."""
+    from hayate_amd.tick_graph import StaticTickBatch
+
+    say("[static tick batch: slot capacity]")
+    q_lens = [256, 64]
+    lens = [6000, 3000]  # deep prefixes: the planner splits the first chunk's tiles
+    w = _custom_workload(32, 8, lens, q_lens, seed=12)
+    m, hs = w.manager, w.handles
+    eager = PagedKVBatch(m, q_lens, list(lens), [list(h.pages) for h in hs], varlen=True,
+                         num_q_heads=32)
+    need = eager.plan(32).host.n_prefill_slots
+    assert need > 0
+    max_tokens = max(c + q for c, q in zip(lens, q_lens))
+    small = StaticTickBatch(m, q_lens, 32, max_tokens=max_tokens, prefill_slots=need - 1)
+    assert not small.refresh(hs) and small.prefill_slots_needed == need
+    big = StaticTickBatch(m, q_lens, 32, max_tokens=max_tokens, prefill_slots=need)
+    assert big.refresh(hs)
+    pre = (m.k_cache.clone(), m.v_cache.clone())
+    outs = []
+    for batch in (eager, big):
+        m.k_cache.copy_(pre[0])
+        m.v_cache.copy_(pre[1])
+        q_rot = batch.norm_rope_write_layer(0, w.q, w.k, w.v, w.q_norm_w, w.k_norm_w, EPS,
+                                            w.cos, w.sin)
+        out = batch.attend_layer(q_rot, 0)
+        torch.cuda.synchronize()
+        outs.append((bits(q_rot), bits(out), layer_bits(m)))
+    (qa, oa, (ka, va)), (qb, ob, (kb, vb)) = outs
+    assert np.array_equal(qa, qb) and np.array_equal(oa, ob)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
