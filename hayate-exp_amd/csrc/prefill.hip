@@ -32,8 +32,9 @@
 // gfx950's 16-byte direct-to-LDS loads (global_load_lds_dwordx4), two tiles
 // ahead of the one being consumed, without passing through registers; one
 // wait and one barrier per tile. The fourth stage keeps a tile's V rows in
-// place while the next tile's first block runs their P V (below). A load instruction writes 64 lanes x 16
-// bytes to consecutive LDS addresses, so the bank-conflict-free layouts are
+// place while the next tile's first block runs their P V (below). A load
+// instruction writes 64 lanes x 16 bytes to consecutive LDS addresses, so
+// the bank-conflict-free layouts are
 // lane permutations instead of padded rows (16-byte units, "chunk" = 8
 // dims):
 //   K: unit(row, chunk) = (row / 16) * 256 + chunk * 16 + row % 16. The
@@ -302,7 +303,7 @@ void prefill_kernel(
   const int k_base = (c >> 4) * 2048 + h * 128 + (c & 15) * 8;
   const int v_base = 512 * (q16 >> 1) + 64 * (q16 & 1) + 32 * ((r16 & 3) >> 1) + 8 * (r16 >> 2) +
                      4 * (r16 & 1);
-  // Block j's K and V rows in the ring: stage (j / 2) % 3, half j % 2.
+  // Block j's K and V rows in the ring: stage (j / 2) % kStages, half j % 2.
   auto k_block = [&](int j) -> const uint16_t * {
     return smem + ((j >> 1) % kStages) * kStage + 4096 * (j & 1) + k_base;
   };
