@@ -310,9 +310,8 @@ int64_t hy_prefill_workspace_bytes(int32_t n_slots, int32_t num_kv_heads,
  * enqueued after this call on the same stream, completes them. A record
  * with q_end <= q_begin (prefill) or num_splits == 0 (merge) is empty and
  * skipped, so a caller can pad both lists to a fixed launch size (a
- * captured graph's). n_prefill
- * (and n_merge of the merge) is at most 65535 (the grid's y limit); more
- * returns HY_EINVAL.
+ * captured graph's). n_prefill (and n_merge of the merge) is at most 65535
+ * (the grid's y limit); more returns HY_EINVAL.
  * Replaces PagedKVBatch.attend_layer (paged_cache.py:62-71) for T > 1.
  */
 int hy_paged_prefill(const void *q, int64_t q_stride_seq, int64_t q_stride_tok,
