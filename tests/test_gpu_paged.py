@@ -596,6 +596,37 @@ def test_random_ticks_deep_prefixes_pages_and_groups(seed):
     assert_attention_close(bits(out), o_exp, f"random deep tick {seed}")
 
 
+def test_maximum_context_last_rope_row():
+    """Qwen3's longest context: rope tables of 40,960 rows (the reference
+    model's max_position_embeddings) and tokens at positions up to 40,959,
+    the tables' last row. A mixed tick (a decode token at position 40,959, a
+    64-token chunk ending there, a short decode) through the append +
+    attention calls, and a decode tick through the fused call against the
+    two calls; pools and rotated q bit-exact, attention within tolerance."""
+    say("[maximum context 40,960]")
+    cache_lens, q_lens = [40_959, 40_896, 10], [1, 64, 1]
+    w = _custom_workload(32, 8, cache_lens, q_lens, seed=21)
+    w.cos, w.sin = compute_rope_params(128, 1_000_000, 40_960, device=DEV)
+    pre_k, pre_v = layer_bits(w.manager)
+    q_rot, out = gpu_step(w)
+    post_k, post_v = layer_bits(w.manager)
+    pk, pv, q_exp, o_exp = oracle_step(w, pre_k, pre_v)
+    assert np.array_equal(bits(q_rot), q_exp), "rotated q differs"
+    assert np.array_equal(post_k, pk) and np.array_equal(post_v, pv), "pools differ"
+    assert_attention_close(bits(out), o_exp, "maximum context, mixed tick")
+
+    cache_lens = [40_959, 10, 20_000]
+    w_a = _custom_workload(32, 8, cache_lens, [1] * 3, seed=22)
+    w_b = _custom_workload(32, 8, cache_lens, [1] * 3, seed=22)
+    for wk in (w_a, w_b):
+        wk.cos, wk.sin = compute_rope_params(128, 1_000_000, 40_960, device=DEV)
+    pre_k, pre_v = layer_bits(w_a.manager)
+    q_f, out_f = _fused_vs_two_calls(w_a, w_b)
+    _, _, q_exp, o_exp = oracle_step(w_a, pre_k, pre_v)
+    assert np.array_equal(bits(q_f), q_exp), "fused: rotated q differs"
+    assert_attention_close(bits(out_f), o_exp, "maximum context, fused decode")
+
+
 def test_few_key_rows_exact_base():
     """Rows that see 1-4 keys (the first tokens of a chunk at offset 0) put
     most weight on one key, so an error in that key's probability shows in
